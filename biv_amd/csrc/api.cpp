@@ -1,0 +1,591 @@
+// The C ABI of include/biv_hip.h: context, uploads (with the repacking into
+// the device planes of common.hpp), the MoE layer, and the forward pass that
+// queues the kernels of kernels.hip on the context's stream.
+#include "../../include/biv_hip.h"
+#include "common.hpp"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using biv::DevMat;
+
+struct biv_hip_weight {
+    DevMat m;
+};
+
+struct biv_hip_experts {
+    DevMat m;
+};
+
+struct biv_hip_moe {
+    const biv_hip_weight *router, *sg, *su, *sd, *gi;
+    const biv_hip_experts *gate, *up, *down;
+    int k, n_expert, E, ff;
+};
+
+namespace {
+
+// Device buffers of one forward, grown to the largest T seen.
+struct Scratch {
+    int cap_T = 0;
+    std::vector<void *> bufs;
+    int8_t *xq = nullptr;
+    float *xd = nullptr, *xs = nullptr;
+    float *logits = nullptr, *glogit = nullptr;
+    float *act = nullptr;
+    int8_t *aq = nullptr;
+    float *ad = nullptr, *as = nullptr;
+    float *y = nullptr;
+    float *h_stage = nullptr, *o_stage = nullptr;
+    biv::Dispatch dp{};
+};
+
+std::string g_create_error;
+
+} // namespace
+
+struct biv_hip_ctx {
+    int device = 0;
+    hipStream_t own = nullptr;
+    hipStream_t stream = nullptr;
+    std::string err;
+    std::vector<void *> allocs;
+    std::vector<biv_hip_weight *> weights;
+    std::vector<biv_hip_experts *> experts;
+    std::vector<biv_hip_moe *> layers;
+    size_t bytes = 0;
+    Scratch sc;
+    // scratch shape: the widest layer seen
+    int sc_E = 0, sc_ff = 0, sc_ne = 0, sc_k = 0;
+};
+
+namespace {
+
+int fail(biv_hip_ctx *ctx, int code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->err = buf;
+    else g_create_error = buf;
+    return code;
+}
+
+int hip_fail(biv_hip_ctx *ctx, hipError_t e, const char *what)
+{
+    return fail(ctx, BIV_HIP_E_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(ctx, call, what)                                                                                \
+    do {                                                                                                        \
+        hipError_t e_ = (call);                                                                                 \
+        if (e_ != hipSuccess) return hip_fail(ctx, e_, what);                                                   \
+    } while (0)
+
+bool block_of(int ty, size_t &be, size_t &bb)
+{
+    switch (ty) {
+    case BIV_GGML_F32: be = 1; bb = 4; return true;
+    case BIV_GGML_F16:
+    case BIV_GGML_BF16: be = 1; bb = 2; return true;
+    case BIV_GGML_Q8_0: be = 32; bb = 34; return true;
+    case BIV_GGML_Q4_K: be = 256; bb = 144; return true;
+    case BIV_GGML_Q6_K: be = 256; bb = 210; return true;
+    default: return false;
+    }
+}
+
+// Types the expert kernels compute with.
+bool expert_type_ok(int ty) { return ty == BIV_GGML_Q8_0 || ty == BIV_GGML_Q4_K || ty == BIV_GGML_Q6_K; }
+
+int dev_alloc(biv_hip_ctx *ctx, size_t bytes, uint8_t **out)
+{
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) return fail(ctx, BIV_HIP_E_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    ctx->allocs.push_back(p);
+    ctx->bytes += bytes;
+    *out = static_cast<uint8_t *>(p);
+    return 0;
+}
+
+// Repack n matrices of rows x cols from ggml rows (matrix e at
+// data + e*stride + offset) into the planes of DevMat.
+int upload_mat(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, const uint8_t *data, size_t stride,
+               size_t offset, DevMat &m)
+{
+    size_t be, bb;
+    if (!block_of(ty, be, bb)) return fail(ctx, BIV_HIP_E_TYPE, "no kernel for ggml type %d", ty);
+    if (cols == 0 || rows == 0 || n == 0 || cols % be)
+        return fail(ctx, BIV_HIP_E_INVALID, "shape %zux%zux%zu does not fit type %d", cols, rows, n, ty);
+    if (!data) return fail(ctx, BIV_HIP_E_INVALID, "null weight data");
+    const size_t row_bytes = cols / be * bb;
+    const size_t nr = n * rows;
+    m.ty = ty;
+    m.cols = (int)cols;
+    m.rows = (int)rows;
+    m.n = (int)n;
+    auto src_row = [&](size_t e, size_t r) { return data + e * stride + offset + r * row_bytes; };
+    size_t qrow = 0, srow = 0, drow = 0;
+    switch (ty) {
+    case BIV_GGML_Q8_0: qrow = cols; srow = cols / 32 * 2; break;
+    case BIV_GGML_Q4_K: qrow = cols / 2; srow = cols / 256 * 16; break;
+    case BIV_GGML_Q6_K: qrow = cols / 256 * 192; srow = cols / 256 * 16; drow = cols / 256 * 2; break;
+    default: qrow = row_bytes; break;
+    }
+    std::vector<uint8_t> q(nr * qrow), s(nr * srow), d(nr * drow);
+    for (size_t e = 0; e < n; e++)
+        for (size_t r = 0; r < rows; r++) {
+            const uint8_t *src = src_row(e, r);
+            const size_t i = e * rows + r;
+            switch (ty) {
+            case BIV_GGML_Q8_0:
+                for (size_t b = 0; b < cols / 32; b++) {
+                    memcpy(&s[i * srow + 2 * b], src + 34 * b, 2);
+                    memcpy(&q[i * qrow + 32 * b], src + 34 * b + 2, 32);
+                }
+                break;
+            case BIV_GGML_Q4_K:
+                for (size_t b = 0; b < cols / 256; b++) {
+                    memcpy(&s[i * srow + 16 * b], src + 144 * b, 16);
+                    memcpy(&q[i * qrow + 128 * b], src + 144 * b + 16, 128);
+                }
+                break;
+            case BIV_GGML_Q6_K:
+                for (size_t b = 0; b < cols / 256; b++) {
+                    memcpy(&q[i * qrow + 192 * b], src + 210 * b, 192);
+                    memcpy(&s[i * srow + 16 * b], src + 210 * b + 192, 16);
+                    memcpy(&d[i * drow + 2 * b], src + 210 * b + 208, 2);
+                }
+                break;
+            default:
+                memcpy(&q[i * qrow], src, row_bytes);
+                break;
+            }
+        }
+    int rc;
+    if ((rc = dev_alloc(ctx, q.size(), &m.q))) return rc;
+    HIP_TRY(ctx, hipMemcpy(m.q, q.data(), q.size(), hipMemcpyHostToDevice), "upload");
+    if (srow) {
+        if ((rc = dev_alloc(ctx, s.size(), &m.s))) return rc;
+        HIP_TRY(ctx, hipMemcpy(m.s, s.data(), s.size(), hipMemcpyHostToDevice), "upload");
+    }
+    if (drow) {
+        if ((rc = dev_alloc(ctx, d.size(), &m.d))) return rc;
+        HIP_TRY(ctx, hipMemcpy(m.d, d.data(), d.size(), hipMemcpyHostToDevice), "upload");
+    }
+    return 0;
+}
+
+template <class T> int sc_alloc(biv_hip_ctx *ctx, size_t count, T **out)
+{
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, count * sizeof(T) + 16);
+    if (e != hipSuccess)
+        return fail(ctx, BIV_HIP_E_NOMEM, "scratch hipMalloc(%zu): %s", count * sizeof(T), hipGetErrorString(e));
+    ctx->sc.bufs.push_back(p);
+    *out = static_cast<T *>(p);
+    return 0;
+}
+
+void scratch_free(biv_hip_ctx *ctx)
+{
+    for (void *p : ctx->sc.bufs) (void)hipFree(p);
+    ctx->sc = Scratch{};
+}
+
+// Make the scratch fit T tokens of layer m.
+int scratch_fit(biv_hip_ctx *ctx, const biv_hip_moe *m, int T)
+{
+    Scratch &s = ctx->sc;
+    if (T <= s.cap_T && m->E <= ctx->sc_E && m->ff <= ctx->sc_ff && m->n_expert <= ctx->sc_ne && m->k <= ctx->sc_k)
+        return 0;
+    // wait for queued work before freeing what it may use
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "sync");
+    scratch_free(ctx);
+    const int cap = T < 16 ? 16 : T;
+    ctx->sc_E = std::max(ctx->sc_E, m->E);
+    ctx->sc_ff = std::max(ctx->sc_ff, m->ff);
+    ctx->sc_ne = std::max(ctx->sc_ne, m->n_expert);
+    ctx->sc_k = std::max(ctx->sc_k, m->k);
+    const size_t E = ctx->sc_E, ff = ctx->sc_ff, ne = ctx->sc_ne, k = ctx->sc_k;
+    const size_t P = (size_t)cap * k, R = P + cap;
+    int rc = 0;
+    rc = rc ? rc : sc_alloc(ctx, cap * E, &s.xq);
+    rc = rc ? rc : sc_alloc(ctx, cap * E / 32, &s.xd);
+    rc = rc ? rc : sc_alloc(ctx, cap * E / 32, &s.xs);
+    rc = rc ? rc : sc_alloc(ctx, cap * ne, &s.logits);
+    rc = rc ? rc : sc_alloc(ctx, (size_t)cap, &s.glogit);
+    rc = rc ? rc : sc_alloc(ctx, R * ff, &s.act);
+    rc = rc ? rc : sc_alloc(ctx, R * ff, &s.aq);
+    rc = rc ? rc : sc_alloc(ctx, R * ff / 32, &s.ad);
+    rc = rc ? rc : sc_alloc(ctx, R * ff / 32, &s.as);
+    rc = rc ? rc : sc_alloc(ctx, R * E, &s.y);
+    rc = rc ? rc : sc_alloc(ctx, cap * E, &s.h_stage);
+    rc = rc ? rc : sc_alloc(ctx, cap * E, &s.o_stage);
+    rc = rc ? rc : sc_alloc(ctx, 1, &s.dp.n_active);
+    rc = rc ? rc : sc_alloc(ctx, ne, &s.dp.act_expert);
+    rc = rc ? rc : sc_alloc(ctx, ne, &s.dp.act_beg);
+    rc = rc ? rc : sc_alloc(ctx, ne, &s.dp.act_cnt);
+    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_tok);
+    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_exp);
+    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_w);
+    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.tok_pairs);
+    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.ids);
+    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.wts);
+    if (rc) {
+        scratch_free(ctx);
+        return rc;
+    }
+    s.cap_T = cap;
+    return 0;
+}
+
+struct Dumps {
+    int32_t *gate = nullptr, *up = nullptr, *down = nullptr;
+};
+
+// Queue the whole block: h and out are device pointers.
+int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float *out, unsigned flags,
+            const Dumps &dm)
+{
+    if (T == 0) return 0;
+    int rc = scratch_fit(ctx, m, T);
+    if (rc) return rc;
+    Scratch &s = ctx->sc;
+    hipStream_t st = ctx->stream;
+    const int E = m->E, ff = m->ff, ne = m->n_expert, k = m->k;
+    const int P = T * k;
+    const bool has_shared = m->sg != nullptr;
+    HIP_TRY(ctx, biv::launch_quant_rows(h, T * E / 32, s.xq, s.xd, s.xs, st), "quantise h");
+    HIP_TRY(ctx,
+            biv::launch_router(reinterpret_cast<const float *>(m->router->m.q),
+                               has_shared ? reinterpret_cast<const float *>(m->gi->m.q) : nullptr, ne, E, h, T,
+                               s.logits, s.glogit, st),
+            "router");
+    HIP_TRY(ctx, biv::launch_route(s.logits, ne, k, T, s.dp.ids, s.dp.wts, st), "route");
+    HIP_TRY(ctx, biv::launch_sort(s.dp.ids, s.dp.wts, ne, k, T, s.dp, st), "dispatch");
+
+    biv::MvArgs a{};
+    a.a = m->gate->m;
+    a.b = m->up->m;
+    if (has_shared) {
+        a.sa = m->sg->m;
+        a.sb = m->su->m;
+    }
+    a.xq = s.xq;
+    a.xd = s.xd;
+    a.xs = s.xs;
+    a.dp = s.dp;
+    a.out = s.act;
+    a.dump_a = dm.gate;
+    a.dump_b = dm.up;
+    a.T = T;
+    a.P = P;
+    a.u_max = std::min(ne, P);
+    a.x_by_token = 1;
+    HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
+
+    const int rows_act = has_shared ? P + T : P;
+    HIP_TRY(ctx, biv::launch_quant_rows(s.act, rows_act * ff / 32, s.aq, s.ad, s.as, st), "quantise act");
+
+    biv::MvArgs d{};
+    d.a = m->down->m;
+    if (has_shared) d.sa = m->sd->m;
+    d.xq = s.aq;
+    d.xd = s.ad;
+    d.xs = s.as;
+    d.dp = s.dp;
+    d.out = s.y;
+    d.dump_a = dm.down;
+    d.T = T;
+    d.P = P;
+    d.u_max = std::min(ne, P);
+    d.x_by_token = 0;
+    HIP_TRY(ctx, biv::launch_down(d, st), "expert down");
+
+    HIP_TRY(ctx,
+            biv::launch_combine(s.y, s.dp, s.glogit, has_shared, T, P, k, E, out, (flags & BIV_HIP_ADD) != 0, st),
+            "combine");
+    return 0;
+}
+
+} // namespace
+
+extern "C" {
+
+int biv_hip_create(int device, biv_hip_ctx **out)
+{
+    if (!out) return fail(nullptr, BIV_HIP_E_INVALID, "null output pointer");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(nullptr, BIV_HIP_E_DEVICE, "no HIP device (%s)", hipGetErrorString(e));
+    if (device < 0 || device >= n) return fail(nullptr, BIV_HIP_E_INVALID, "device %d of %d", device, n);
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return fail(nullptr, BIV_HIP_E_DEVICE, "device properties: %s", hipGetErrorString(e));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(nullptr, BIV_HIP_E_DEVICE, "device %d is %s; this library is built for gfx950", device,
+                    prop.gcnArchName);
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return fail(nullptr, BIV_HIP_E_DEVICE, "hipSetDevice: %s", hipGetErrorString(e));
+    auto *ctx = new biv_hip_ctx();
+    ctx->device = device;
+    e = hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return fail(nullptr, BIV_HIP_E_DEVICE, "stream: %s", hipGetErrorString(e));
+    }
+    ctx->stream = ctx->own;
+    *out = ctx;
+    return 0;
+}
+
+void biv_hip_destroy(biv_hip_ctx *ctx)
+{
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    scratch_free(ctx);
+    for (void *p : ctx->allocs) (void)hipFree(p);
+    for (auto *w : ctx->weights) delete w;
+    for (auto *x : ctx->experts) delete x;
+    for (auto *l : ctx->layers) delete l;
+    if (ctx->own) (void)hipStreamDestroy(ctx->own);
+    delete ctx;
+}
+
+const char *biv_hip_last_error(const biv_hip_ctx *ctx) { return ctx ? ctx->err.c_str() : g_create_error.c_str(); }
+
+int biv_hip_set_stream(biv_hip_ctx *ctx, void *stream)
+{
+    if (!ctx) return BIV_HIP_E_INVALID;
+    ctx->stream = stream ? static_cast<hipStream_t>(stream) : ctx->own;
+    return 0;
+}
+
+int biv_hip_sync(biv_hip_ctx *ctx)
+{
+    if (!ctx) return BIV_HIP_E_INVALID;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "sync");
+    return 0;
+}
+
+int biv_hip_upload_weight(biv_hip_ctx *ctx, int ggml_type, size_t cols, size_t rows, const void *data,
+                          biv_hip_weight **out)
+{
+    if (!ctx || !out) return BIV_HIP_E_INVALID;
+    HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    auto *w = new biv_hip_weight();
+    int rc = upload_mat(ctx, ggml_type, cols, rows, 1, static_cast<const uint8_t *>(data), 0, 0, w->m);
+    if (rc) {
+        delete w;
+        return rc;
+    }
+    ctx->weights.push_back(w);
+    *out = w;
+    return 0;
+}
+
+int biv_hip_upload_experts(biv_hip_ctx *ctx, int ggml_type, size_t cols, size_t rows, size_t n_expert,
+                           const void *data, size_t stride, size_t offset, biv_hip_experts **out)
+{
+    if (!ctx || !out) return BIV_HIP_E_INVALID;
+    HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    size_t be, bb;
+    if (!block_of(ggml_type, be, bb)) return fail(ctx, BIV_HIP_E_TYPE, "no kernel for ggml type %d", ggml_type);
+    if (cols % be == 0 && stride < offset + rows * (cols / be * bb) && n_expert > 1)
+        return fail(ctx, BIV_HIP_E_INVALID, "expert stride %zu is smaller than a matrix", stride);
+    auto *x = new biv_hip_experts();
+    int rc = upload_mat(ctx, ggml_type, cols, rows, n_expert, static_cast<const uint8_t *>(data), stride, offset,
+                        x->m);
+    if (rc) {
+        delete x;
+        return rc;
+    }
+    ctx->experts.push_back(x);
+    *out = x;
+    return 0;
+}
+
+int biv_hip_moe_create(biv_hip_ctx *ctx, const biv_hip_weight *router, const biv_hip_experts *gate,
+                       const biv_hip_experts *up, const biv_hip_experts *down, const biv_hip_weight *shared_gate,
+                       const biv_hip_weight *shared_up, const biv_hip_weight *shared_down,
+                       const biv_hip_weight *gate_inp, int k, biv_hip_moe **out)
+{
+    if (!ctx || !out) return BIV_HIP_E_INVALID;
+    if (!router || !gate || !up || !down) return fail(ctx, BIV_HIP_E_INVALID, "router and experts are required");
+    const int n_shared = !!shared_gate + !!shared_up + !!shared_down + !!gate_inp;
+    if (n_shared != 0 && n_shared != 4)
+        return fail(ctx, BIV_HIP_E_INVALID, "the shared expert needs gate, up, down and gate_inp");
+    const DevMat &g = gate->m, &u = up->m, &d = down->m, &r = router->m;
+    const int E = g.cols, ff = g.rows, ne = g.n;
+    if (r.ty != BIV_GGML_F32) return fail(ctx, BIV_HIP_E_TYPE, "router type %d: only F32 routers", r.ty);
+    if (!expert_type_ok(g.ty) || !expert_type_ok(u.ty) || !expert_type_ok(d.ty))
+        return fail(ctx, BIV_HIP_E_TYPE, "expert types %d/%d/%d: kernels exist for Q8_0, Q4_K, Q6_K", g.ty, u.ty,
+                    d.ty);
+    if (g.ty != u.ty) return fail(ctx, BIV_HIP_E_TYPE, "gate and up experts must share a type");
+    if (u.cols != E || u.rows != ff || u.n != ne || d.cols != ff || d.rows != E || d.n != ne)
+        return fail(ctx, BIV_HIP_E_INVALID, "expert shapes disagree: gate %dx%dx%d up %dx%dx%d down %dx%dx%d", g.cols,
+                    g.rows, g.n, u.cols, u.rows, u.n, d.cols, d.rows, d.n);
+    if (r.cols != E || r.rows != ne) return fail(ctx, BIV_HIP_E_INVALID, "router is %dx%d, want %dx%d", r.cols, r.rows, E, ne);
+    auto width_ok = [](int K) { return K == 512 || K == 1024 || K == 2048; };
+    if (!width_ok(E) || !width_ok(ff))
+        return fail(ctx, BIV_HIP_E_INVALID, "n_embd %d / n_ff %d: the matvec kernels take 512, 1024 or 2048", E, ff);
+    if (ne > 256) return fail(ctx, BIV_HIP_E_INVALID, "%d experts: at most 256", ne);
+    if (k < 1 || k > 16 || k > ne) return fail(ctx, BIV_HIP_E_INVALID, "k = %d not in 1..min(16, n_expert)", k);
+    if (n_shared) {
+        const DevMat &sg = shared_gate->m, &su = shared_up->m, &sd = shared_down->m, &gi = gate_inp->m;
+        if (!expert_type_ok(sg.ty) || !expert_type_ok(su.ty) || !expert_type_ok(sd.ty) || sg.ty != su.ty)
+            return fail(ctx, BIV_HIP_E_TYPE, "shared expert types %d/%d/%d", sg.ty, su.ty, sd.ty);
+        if (gi.ty != BIV_GGML_F32) return fail(ctx, BIV_HIP_E_TYPE, "gate_inp type %d: only F32", gi.ty);
+        if (sg.cols != E || su.cols != E || sd.rows != E || sg.rows != ff || su.rows != ff || sd.cols != ff ||
+            gi.cols != E || gi.rows != 1)
+            return fail(ctx, BIV_HIP_E_INVALID, "shared expert must be %dx%d (gate/up), %dx%d (down), gate_inp %d", E,
+                        ff, ff, E, E);
+    }
+    auto *m = new biv_hip_moe();
+    m->router = router;
+    m->gate = gate;
+    m->up = up;
+    m->down = down;
+    m->sg = shared_gate;
+    m->su = shared_up;
+    m->sd = shared_down;
+    m->gi = gate_inp;
+    m->k = k;
+    m->n_expert = ne;
+    m->E = E;
+    m->ff = ff;
+    ctx->layers.push_back(m);
+    *out = m;
+    return 0;
+}
+
+static int check_fwd(biv_hip_ctx *ctx, const biv_hip_moe *moe, const void *h, int n, const void *out)
+{
+    if (!ctx) return BIV_HIP_E_INVALID;
+    if (!moe) return fail(ctx, BIV_HIP_E_INVALID, "null layer");
+    if (n < 0) return fail(ctx, BIV_HIP_E_INVALID, "n = %d", n);
+    if (n > 0 && (!h || !out)) return fail(ctx, BIV_HIP_E_INVALID, "null h or out");
+    if ((long long)n * moe->k >= (1 << 20)) return fail(ctx, BIV_HIP_E_INVALID, "n * k = %lld pairs: too many", (long long)n * moe->k);
+    return 0;
+}
+
+int biv_hip_moe_forward_device(biv_hip_ctx *ctx, const biv_hip_moe *moe, const float *h_dev, int n, float *out_dev,
+                               unsigned flags)
+{
+    int rc = check_fwd(ctx, moe, h_dev, n, out_dev);
+    if (rc) return rc;
+    HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    return forward(ctx, moe, h_dev, n, out_dev, flags, Dumps{});
+}
+
+int biv_hip_moe_forward_taps(biv_hip_ctx *ctx, const biv_hip_moe *moe, const float *h, int n, float *out,
+                             unsigned flags, const biv_hip_taps *taps)
+{
+    int rc = check_fwd(ctx, moe, h, n, out);
+    if (rc) return rc;
+    if (n == 0) return 0;
+    HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    if ((rc = scratch_fit(ctx, moe, n))) return rc;
+    Scratch &s = ctx->sc;
+    const size_t E = moe->E, ff = moe->ff, k = moe->k, P = (size_t)n * k, R = P + n;
+    HIP_TRY(ctx, hipMemcpyAsync(s.h_stage, h, sizeof(float) * n * E, hipMemcpyHostToDevice, ctx->stream), "copy h");
+    if (flags & BIV_HIP_ADD)
+        HIP_TRY(ctx, hipMemcpyAsync(s.o_stage, out, sizeof(float) * n * E, hipMemcpyHostToDevice, ctx->stream),
+                "copy x");
+    Dumps dm;
+    std::vector<void *> tmp;
+    auto dev = [&](size_t bytes) -> int32_t * {
+        void *p = nullptr;
+        if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+        tmp.push_back(p);
+        return static_cast<int32_t *>(p);
+    };
+    if (taps && taps->gate_idots) dm.gate = dev(sizeof(int32_t) * R * ff * (E / 32));
+    if (taps && taps->up_idots) dm.up = dev(sizeof(int32_t) * R * ff * (E / 32));
+    if (taps && taps->down_idots) dm.down = dev(sizeof(int32_t) * R * E * (ff / 32));
+    rc = forward(ctx, moe, s.h_stage, n, s.o_stage, flags, dm);
+    auto d2h = [&](void *dst, const void *src, size_t bytes) {
+        if (!rc && dst && src) {
+            hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+            if (e != hipSuccess) rc = hip_fail(ctx, e, "copy taps");
+        }
+    };
+    d2h(out, s.o_stage, sizeof(float) * n * E);
+    if (taps) {
+        d2h(taps->ids, s.dp.ids, sizeof(int32_t) * P);
+        d2h(taps->weights, s.dp.wts, sizeof(float) * P);
+        d2h(taps->logits, s.logits, sizeof(float) * n * moe->n_expert);
+        d2h(taps->shared_logit, moe->sg ? s.glogit : nullptr, sizeof(float) * n);
+        d2h(taps->pair_token, s.dp.pair_tok, sizeof(int32_t) * P);
+        d2h(taps->pair_expert, s.dp.pair_exp, sizeof(int32_t) * P);
+        d2h(taps->gate_idots, dm.gate, sizeof(int32_t) * R * ff * (E / 32));
+        d2h(taps->up_idots, dm.up, sizeof(int32_t) * R * ff * (E / 32));
+        d2h(taps->act_q, s.aq, R * ff);
+        d2h(taps->act_d, s.ad, sizeof(float) * R * ff / 32);
+        d2h(taps->down_idots, dm.down, sizeof(int32_t) * R * E * (ff / 32));
+    }
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    for (void *p : tmp) (void)hipFree(p);
+    if (!rc && e != hipSuccess) rc = hip_fail(ctx, e, "forward");
+    return rc;
+}
+
+int biv_hip_moe_forward(biv_hip_ctx *ctx, const biv_hip_moe *moe, const float *h, int n, float *out, unsigned flags)
+{
+    return biv_hip_moe_forward_taps(ctx, moe, h, n, out, flags, nullptr);
+}
+
+int biv_hip_malloc(biv_hip_ctx *ctx, size_t bytes, void **out)
+{
+    if (!ctx || !out) return BIV_HIP_E_INVALID;
+    HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+    if (e != hipSuccess) return fail(ctx, BIV_HIP_E_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    return 0;
+}
+
+int biv_hip_free(biv_hip_ctx *ctx, void *p)
+{
+    if (!ctx) return BIV_HIP_E_INVALID;
+    HIP_TRY(ctx, hipFree(p), "hipFree");
+    return 0;
+}
+
+int biv_hip_memcpy_h2d(biv_hip_ctx *ctx, void *dst, const void *src, size_t bytes)
+{
+    if (!ctx) return BIV_HIP_E_INVALID;
+    HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "h2d");
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "h2d");
+    return 0;
+}
+
+int biv_hip_memcpy_d2h(biv_hip_ctx *ctx, void *dst, const void *src, size_t bytes)
+{
+    if (!ctx) return BIV_HIP_E_INVALID;
+    HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "d2h");
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "d2h");
+    return 0;
+}
+
+int biv_hip_numerics(const biv_hip_ctx *ctx, char *buf, size_t len)
+{
+    if (!buf || len == 0) return BIV_HIP_E_INVALID;
+    snprintf(buf, len,
+             "kind=hip;arch=gfx950;act=q8_32_f32scale;router=f32_avx2_order;route=softmax_topk_lowidx;"
+             "experts=int32_block_dot_f32_scale;combine=fma_ascending_expert;deterministic=1");
+    return 0;
+}
+
+size_t biv_hip_device_bytes(const biv_hip_ctx *ctx) { return ctx ? ctx->bytes : 0; }
+
+} // extern "C"

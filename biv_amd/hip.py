@@ -1,0 +1,224 @@
+"""Host side of the gfx950 MoE backend, over the C ABI of include/biv_hip.h.
+
+This mirrors the interface biv's MoE path sits behind: a backend context
+(Engine construction, engine/src/engine.rs:15-60), weights uploaded once
+(Weight / Experts, engine/src/ops.rs:12-43, model.rs:190-217), a MoE layer
+(struct Moe, model.rs:229-237) and `ffn(h, n)` (Model::ffn, model.rs:853-898)
+returning the block's output for n tokens.  Errors come back as HipError with
+the library's message, as biv's backends return Error::Backend(String)
+(engine/src/error.rs:67-68).
+
+The library is required: there is no CPU fallback.  If libbiv_hip.so is not
+built, loading raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+from . import synth
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbiv_hip.so")
+
+ADD = 1
+
+# every symbol include/biv_hip.h declares
+SYMBOLS = [
+    "biv_hip_create", "biv_hip_destroy", "biv_hip_last_error", "biv_hip_set_stream", "biv_hip_sync",
+    "biv_hip_upload_weight", "biv_hip_upload_experts", "biv_hip_moe_create", "biv_hip_moe_forward",
+    "biv_hip_moe_forward_device", "biv_hip_moe_forward_taps", "biv_hip_malloc", "biv_hip_free",
+    "biv_hip_memcpy_h2d", "biv_hip_memcpy_d2h", "biv_hip_numerics", "biv_hip_device_bytes",
+]
+
+
+class HipError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"biv_hip error {code}: {msg}")
+        self.code = code
+
+
+class Taps(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "ids", "weights", "logits", "shared_logit", "pair_token", "pair_expert", "gate_idots", "up_idots",
+        "act_q", "act_d", "down_idots")]
+
+
+_lib = None
+
+
+def load():
+    """The loaded libbiv_hip.so; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise HipError(-3, f"{LIB_PATH} is not built (python -m biv_amd.build)")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    pp = ctypes.POINTER(ctypes.c_void_p)
+    L.biv_hip_create.argtypes = [i, pp]
+    L.biv_hip_destroy.argtypes = [vp]
+    L.biv_hip_destroy.restype = None
+    L.biv_hip_last_error.argtypes = [vp]
+    L.biv_hip_last_error.restype = ctypes.c_char_p
+    L.biv_hip_set_stream.argtypes = [vp, vp]
+    L.biv_hip_sync.argtypes = [vp]
+    L.biv_hip_upload_weight.argtypes = [vp, i, sz, sz, vp, pp]
+    L.biv_hip_upload_experts.argtypes = [vp, i, sz, sz, sz, vp, sz, sz, pp]
+    L.biv_hip_moe_create.argtypes = [vp] + [vp] * 8 + [i, pp]
+    L.biv_hip_moe_forward.argtypes = [vp, vp, vp, i, vp, ctypes.c_uint]
+    L.biv_hip_moe_forward_device.argtypes = [vp, vp, vp, i, vp, ctypes.c_uint]
+    L.biv_hip_moe_forward_taps.argtypes = [vp, vp, vp, i, vp, ctypes.c_uint, ctypes.POINTER(Taps)]
+    L.biv_hip_malloc.argtypes = [vp, sz, pp]
+    L.biv_hip_free.argtypes = [vp, vp]
+    L.biv_hip_memcpy_h2d.argtypes = [vp, vp, vp, sz]
+    L.biv_hip_memcpy_d2h.argtypes = [vp, vp, vp, sz]
+    L.biv_hip_numerics.argtypes = [vp, ctypes.c_char_p, sz]
+    L.biv_hip_device_bytes.argtypes = [vp]
+    L.biv_hip_device_bytes.restype = sz
+    _lib = L
+    return L
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+class HipMoe:
+    """A MoE layer on the device: the counterpart of model::Moe."""
+
+    def __init__(self, ctx, handle, layer):
+        self.ctx = ctx
+        self.handle = handle
+        self.n_embd = layer.n_embd
+        self.n_expert = layer.n_expert
+        self.k = layer.k
+        self.n_ff = layer.n_ff
+        self.has_shared = layer.shared is not None
+
+    def ffn(self, h, n=None, out=None, add=False):
+        """Model::ffn for a MoE layer (model.rs:853-898): the block's output for
+        the n tokens of h [n x n_embd]; with add=True, out += the block."""
+        h = np.ascontiguousarray(h, dtype=np.float32).reshape(-1, self.n_embd)
+        n = h.shape[0] if n is None else n
+        if out is None:
+            out = np.zeros((n, self.n_embd), np.float32)
+        self.ctx._check(self.ctx.L.biv_hip_moe_forward(self.ctx.h, self.handle, _ptr(h), n, _ptr(out),
+                                                       ADD if add else 0))
+        return out
+
+    def ffn_taps(self, h, add=False, out=None, dots=True):
+        """ffn with the debug taps: returns (out, dict of taps); dots=False
+        skips the per-block int32 taps (large at prefill sizes)."""
+        h = np.ascontiguousarray(h, dtype=np.float32).reshape(-1, self.n_embd)
+        n, k, E, ff = h.shape[0], self.k, self.n_embd, self.n_ff
+        P, R = n * k, n * k + n
+        t = dict(
+            ids=np.zeros((n, k), np.int32), weights=np.zeros((n, k), np.float32),
+            logits=np.zeros((n, self.n_expert), np.float32), shared_logit=np.zeros(n, np.float32),
+            pair_token=np.zeros(P, np.int32), pair_expert=np.zeros(P, np.int32),
+            gate_idots=np.zeros((R, ff, E // 32), np.int32) if dots else None,
+            up_idots=np.zeros((R, ff, E // 32), np.int32) if dots else None,
+            act_q=np.zeros((R, ff), np.int8), act_d=np.zeros((R, ff // 32), np.float32),
+            down_idots=np.zeros((R, E, ff // 32), np.int32) if dots else None)
+        if not dots:
+            for name in ("gate_idots", "up_idots", "down_idots"):
+                t[name] = None
+        taps = Taps(**{name: (arr.ctypes.data if arr is not None else None) for name, arr in t.items()})
+        if out is None:
+            out = np.zeros((n, E), np.float32)
+        self.ctx._check(self.ctx.L.biv_hip_moe_forward_taps(self.ctx.h, self.handle, _ptr(h), n, _ptr(out),
+                                                            ADD if add else 0, ctypes.byref(taps)))
+        return out, t
+
+    def forward_device(self, h_dev, n, out_dev, add=False):
+        """encode_moe's counterpart: device pointers, queued on the context's stream."""
+        self.ctx._check(self.ctx.L.biv_hip_moe_forward_device(self.ctx.h, self.handle, ctypes.c_void_p(h_dev), n,
+                                                              ctypes.c_void_p(out_dev), ADD if add else 0))
+
+
+class HipEngine:
+    """A context on one GPU: owns the uploads, the scratch and the stream."""
+
+    def __init__(self, device=0):
+        self.L = load()
+        h = ctypes.c_void_p()
+        rc = self.L.biv_hip_create(device, ctypes.byref(h))
+        if rc:
+            raise HipError(rc, self.L.biv_hip_last_error(None).decode())
+        self.h = h
+        self._keep = []
+
+    def _check(self, rc):
+        if rc:
+            raise HipError(rc, self.L.biv_hip_last_error(self.h).decode())
+
+    def close(self):
+        if self.h:
+            self.L.biv_hip_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def upload_weight(self, w):
+        out = ctypes.c_void_p()
+        self._check(self.L.biv_hip_upload_weight(self.h, w.ty, w.cols, w.rows, _ptr(w.data), ctypes.byref(out)))
+        return out
+
+    def upload_experts(self, x):
+        out = ctypes.c_void_p()
+        self._check(self.L.biv_hip_upload_experts(self.h, x.ty, x.cols, x.rows, x.n, _ptr(x.data), x.stride,
+                                                  x.offset, ctypes.byref(out)))
+        return out
+
+    def moe(self, layer: "synth.MoeLayer"):
+        """Upload a layer's parts and make the device MoE block."""
+        router = self.upload_weight(layer.router)
+        gate, up, down = (self.upload_experts(x) for x in (layer.gate, layer.up, layer.down))
+        sh = [None] * 4
+        if layer.shared is not None:
+            sh = [self.upload_weight(w) for w in layer.shared]
+        out = ctypes.c_void_p()
+        self._check(self.L.biv_hip_moe_create(self.h, router, gate, up, down, *sh, layer.k, ctypes.byref(out)))
+        return HipMoe(self, out, layer)
+
+    def set_stream(self, stream_ptr):
+        self._check(self.L.biv_hip_set_stream(self.h, ctypes.c_void_p(stream_ptr)))
+
+    def sync(self):
+        self._check(self.L.biv_hip_sync(self.h))
+
+    def malloc(self, nbytes):
+        p = ctypes.c_void_p()
+        self._check(self.L.biv_hip_malloc(self.h, nbytes, ctypes.byref(p)))
+        return p.value
+
+    def free(self, p):
+        self._check(self.L.biv_hip_free(self.h, ctypes.c_void_p(p)))
+
+    def h2d(self, dst, arr):
+        arr = np.ascontiguousarray(arr)
+        self._check(self.L.biv_hip_memcpy_h2d(self.h, ctypes.c_void_p(dst), _ptr(arr), arr.nbytes))
+
+    def d2h(self, arr, src):
+        self._check(self.L.biv_hip_memcpy_d2h(self.h, _ptr(arr), ctypes.c_void_p(src), arr.nbytes))
+        return arr
+
+    def numerics(self):
+        buf = ctypes.create_string_buffer(512)
+        self._check(self.L.biv_hip_numerics(self.h, buf, 512))
+        return dict(kv.split("=", 1) for kv in buf.value.decode().split(";") if kv)
+
+    def device_bytes(self):
+        return self.L.biv_hip_device_bytes(self.h)

@@ -1,0 +1,159 @@
+/* biv_hip.h — C ABI of the MI355X (gfx950) backend for biv's qwen35moe
+ * mixture-of-experts feed-forward block.
+ *
+ * The library replaces, for one GPU, the MoE block that biv computes on the
+ * CPU in Model::moe (engine/src/model.rs:860-898) and on Metal in
+ * MetalEngine::encode_moe (engine/src/metal/mod.rs:2138-2266).  A Rust
+ * `hip` backend binds these functions through `extern "C"`; the binding a
+ * maintainer adds is shown in INTEGRATION.md.
+ *
+ * Conventions
+ *  - Every function returns 0 on success and a negative BIV_HIP_E_* code on
+ *    failure; biv_hip_last_error() then describes it.  This maps onto
+ *    Error::Backend(String) (engine/src/error.rs:67-68).
+ *  - Weights are copied into device memory at upload (biv borrows them from
+ *    the mmap'd GGUF, engine/src/ops.rs:14-20; the GPU needs its own copy).
+ *    The context owns every upload and frees it in biv_hip_destroy.
+ *  - A context is used by one host thread at a time and runs all of its work
+ *    on one HIP stream, in submission order.  It takes no locks.  biv's
+ *    Engine is not Send/Sync either (engine/src/batch.rs:1-20).
+ *  - Results are deterministic: the same inputs give the same bits on every
+ *    run (no floating-point atomics; fixed reduction and combine orders).
+ */
+#ifndef BIV_HIP_H
+#define BIV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml tensor types (engine/src/quant.rs:31-48).  The MoE path computes with
+ * F32 (router, shared gate), Q8_0, Q4_K, Q6_K and BF16 (experts). */
+enum {
+    BIV_GGML_F32 = 0,
+    BIV_GGML_F16 = 1,
+    BIV_GGML_Q8_0 = 8,
+    BIV_GGML_Q4_K = 12,
+    BIV_GGML_Q6_K = 14,
+    BIV_GGML_BF16 = 30,
+};
+
+enum {
+    BIV_HIP_OK = 0,
+    BIV_HIP_E_INVALID = -1, /* bad argument or shape (Error::TensorShape, model.rs:332-340) */
+    BIV_HIP_E_TYPE = -2,    /* no kernel for this type (Error::NoKernel, model.rs:341-346) */
+    BIV_HIP_E_DEVICE = -3,  /* HIP runtime failure */
+    BIV_HIP_E_NOMEM = -4,   /* device allocation failed (Error::OutOfMemory) */
+};
+
+/* forward flags */
+enum {
+    BIV_HIP_ADD = 1, /* x += moe(h), as the caller of Model::ffn does (model.rs:788-790) */
+};
+
+typedef struct biv_hip_ctx biv_hip_ctx;
+typedef struct biv_hip_weight biv_hip_weight;
+typedef struct biv_hip_experts biv_hip_experts;
+typedef struct biv_hip_moe biv_hip_moe;
+
+/* A context on HIP device `device` with its own stream.  Replaces the
+ * backend construction of MetalEngine::new (engine/src/metal/mod.rs:610-686). */
+int biv_hip_create(int device, biv_hip_ctx **out);
+
+/* Frees every weight, layer and scratch buffer of the context. */
+void biv_hip_destroy(biv_hip_ctx *ctx);
+
+/* The last error of the context, or of the last failed biv_hip_create when
+ * ctx is NULL.  Valid until the next call on the context. */
+const char *biv_hip_last_error(const biv_hip_ctx *ctx);
+
+/* Run the context's work on an existing stream (a hipStream_t, e.g. the one
+ * a caller times with events) instead of its own; NULL restores its own. */
+int biv_hip_set_stream(biv_hip_ctx *ctx, void *stream);
+
+/* Wait for all work submitted on the context's stream. */
+int biv_hip_sync(biv_hip_ctx *ctx);
+
+/* Upload one matrix of `rows` rows of `cols` elements in ggml layout
+ * (Weight::new, engine/src/ops.rs:22-33): `data` holds rows * row_size(cols)
+ * bytes on the host.  Used for the router, the shared expert and its gate. */
+int biv_hip_upload_weight(biv_hip_ctx *ctx, int ggml_type, size_t cols, size_t rows, const void *data,
+                          biv_hip_weight **out);
+
+/* Upload a stack of `n_expert` matrices of `rows` x `cols`: expert e's matrix
+ * starts at data + e * stride + offset (Experts::expert, model.rs:207-216;
+ * offset selects the up half of a fused ffn_gate_up_exps, model.rs:389-399).
+ * `data` is host memory of at least (n_expert - 1) * stride + offset +
+ * rows * row_size(cols) bytes. */
+int biv_hip_upload_experts(biv_hip_ctx *ctx, int ggml_type, size_t cols, size_t rows, size_t n_expert,
+                           const void *data, size_t stride, size_t offset, biv_hip_experts **out);
+
+/* A MoE block (struct Moe, model.rs:229-237) from uploaded parts: router
+ * [n_expert x n_embd] (F32), gate/up [n_ff x n_embd] and down [n_embd x n_ff]
+ * expert stacks, and the shared expert (gate, up, down, gate_inp) or four
+ * NULLs for none.  k = experts per token (n_expert_used).  The layer keeps
+ * pointers to the parts, which must outlive it. */
+int biv_hip_moe_create(biv_hip_ctx *ctx, const biv_hip_weight *router, const biv_hip_experts *gate,
+                       const biv_hip_experts *up, const biv_hip_experts *down, const biv_hip_weight *shared_gate,
+                       const biv_hip_weight *shared_up, const biv_hip_weight *shared_down,
+                       const biv_hip_weight *gate_inp, int k, biv_hip_moe **out);
+
+/* The block over n tokens: h is [n x n_embd] f32, already normalised (the h of
+ * Model::layer, model.rs:788).  out = moe(h), or out += moe(h) with
+ * BIV_HIP_ADD.  Host pointers; returns when out is written.  Same result as
+ * Model::ffn for a MoE layer (model.rs:853-898). */
+int biv_hip_moe_forward(biv_hip_ctx *ctx, const biv_hip_moe *moe, const float *h, int n, float *out,
+                        unsigned flags);
+
+/* As biv_hip_moe_forward with device pointers, queued on the context's stream
+ * without waiting: the counterpart of encode_moe (metal/mod.rs:2138-2148),
+ * which adds into the residual buffer x when flags has BIV_HIP_ADD. */
+int biv_hip_moe_forward_device(biv_hip_ctx *ctx, const biv_hip_moe *moe, const float *h_dev, int n, float *out_dev,
+                               unsigned flags);
+
+/* Debug taps of one forward, host buffers, each optional (NULL to skip).
+ * P = n * k routed pairs, in dispatch order: grouped by expert in ascending
+ * id, tokens ascending within an expert (the `routed` lists of model.rs:866-873).
+ * Rows P .. P + n - 1 of the *_idots and act_* taps are the shared expert's,
+ * one per token. */
+typedef struct biv_hip_taps {
+    int32_t *ids;         /* [n x k] chosen experts, in rank order (route, model.rs:256-268) */
+    float *weights;       /* [n x k] their weights */
+    float *logits;        /* [n x n_expert] router logits */
+    float *shared_logit;  /* [n] gate_inp logit of each token */
+    int32_t *pair_token;  /* [P] token of each pair in dispatch order */
+    int32_t *pair_expert; /* [P] expert of each pair in dispatch order */
+    int32_t *gate_idots;  /* [P + n][n_ff][n_embd / 32] int32 dot of every 32-element block */
+    int32_t *up_idots;    /* [P + n][n_ff][n_embd / 32] */
+    int8_t *act_q;        /* [P + n][n_ff] the quantised SwiGLU intermediate */
+    float *act_d;         /* [P + n][n_ff / 32] its block scales */
+    int32_t *down_idots;  /* [P + n][n_embd][n_ff / 32] */
+} biv_hip_taps;
+
+/* biv_hip_moe_forward with the debug kernels' taps: the same kernels,
+ * instantiated to also store what `taps` asks for.  Host pointers. */
+int biv_hip_moe_forward_taps(biv_hip_ctx *ctx, const biv_hip_moe *moe, const float *h, int n, float *out,
+                             unsigned flags, const biv_hip_taps *taps);
+
+/* Device memory helpers for callers without another allocator. */
+int biv_hip_malloc(biv_hip_ctx *ctx, size_t bytes, void **out);
+int biv_hip_free(biv_hip_ctx *ctx, void *p);
+int biv_hip_memcpy_h2d(biv_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+int biv_hip_memcpy_d2h(biv_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* Name/value pairs of what decides the numbers (Engine::numerics,
+ * engine/src/engine.rs:42-46), as "name=value;..." into buf. */
+int biv_hip_numerics(const biv_hip_ctx *ctx, char *buf, size_t len);
+
+/* Bytes of device memory held by the context's uploads (Engine::device_memory,
+ * engine/src/engine.rs:36-40). */
+size_t biv_hip_device_bytes(const biv_hip_ctx *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BIV_HIP_H */

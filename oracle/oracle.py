@@ -1,0 +1,271 @@
+"""ctypes view of the CPU oracle (oracle/_build/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker or the timed CPU baseline,
+never as the product path.  See oracle.c for the reference functions each
+entry restates.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+
+F32, F16, Q8_0, Q4K, Q6K, BF16 = 0, 1, 8, 12, 14, 30
+SCALAR, AVX2, VNNI, AUTO = 0, 1, 2, -1
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_i8p = ctypes.POINTER(ctypes.c_int8)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_f32p = ctypes.POINTER(ctypes.c_float)
+
+
+class OrcWeight(ctypes.Structure):
+    _fields_ = [("ty", ctypes.c_int32), ("pad", ctypes.c_int32), ("data", ctypes.c_void_p)]
+
+
+class OrcExperts(ctypes.Structure):
+    _fields_ = [("ty", ctypes.c_int32), ("pad", ctypes.c_int32), ("data", ctypes.c_void_p),
+                ("stride", ctypes.c_uint64), ("offset", ctypes.c_uint64)]
+
+
+class OrcMoe(ctypes.Structure):
+    _fields_ = [("n_expert", ctypes.c_int32), ("k", ctypes.c_int32), ("n_embd", ctypes.c_int32),
+                ("n_ff", ctypes.c_int32), ("n_ff_sh", ctypes.c_int32), ("pad", ctypes.c_int32),
+                ("router", OrcWeight), ("gate", OrcExperts), ("up", OrcExperts), ("down", OrcExperts),
+                ("sh_gate", OrcWeight), ("sh_up", OrcWeight), ("sh_down", OrcWeight),
+                ("gate_inp", OrcWeight)]
+
+
+def build():
+    """Compile the oracle with its Makefile (gcc)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle not built: {LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(LIB_PATH)
+        L.orc_f16_to_f32.restype = ctypes.c_float
+        L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_bf16_to_f32.restype = ctypes.c_float
+        L.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_row_size.restype = ctypes.c_size_t
+        L.orc_row_size.argtypes = [ctypes.c_int, ctypes.c_size_t]
+        L.orc_dequantize_row.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+        L.orc_q8act_quantize.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+        L.orc_block_idots.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                      ctypes.c_void_p]
+        L.orc_block_idots_rows.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                           ctypes.c_size_t, ctypes.c_void_p]
+        L.orc_dot.restype = ctypes.c_float
+        L.orc_dot.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                              ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        L.orc_dot_f32.restype = ctypes.c_float
+        L.orc_dot_f32.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        L.orc_axpy.argtypes = [ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        L.orc_matmul.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
+                                 ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+        L.orc_softmax.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+        L.orc_sigmoid.restype = ctypes.c_float
+        L.orc_sigmoid.argtypes = [ctypes.c_float]
+        L.orc_silu.restype = ctypes.c_float
+        L.orc_silu.argtypes = [ctypes.c_float]
+        L.orc_rms_norm.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
+                                   ctypes.c_float, ctypes.c_int]
+        L.orc_route.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_void_p,
+                                ctypes.c_void_p]
+        L.orc_dense_ffn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                    ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_void_p,
+                                    ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+        L.orc_moe.argtypes = [ctypes.POINTER(OrcMoe), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                              ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        L.orc_detect_level.restype = ctypes.c_int
+        L.orc_max_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def detect_level():
+    return lib().orc_detect_level()
+
+
+def max_threads():
+    return lib().orc_max_threads()
+
+
+def f16_to_f32(h):
+    return lib().orc_f16_to_f32(h)
+
+
+def bf16_to_f32(h):
+    return lib().orc_bf16_to_f32(h)
+
+
+def row_size(ty, n):
+    return lib().orc_row_size(ty, n)
+
+
+def dequantize_row(ty, w, n):
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    out = np.empty(n, np.float32)
+    if lib().orc_dequantize_row(ty, _p(w), _p(out), n):
+        raise ValueError(f"no dequantisation for type {ty}")
+    return out
+
+
+def q8act(x):
+    """Q8Act::quantize: (qs int8 [n], d f32 [n/32], s f32 [n/32])."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    n = x.size
+    qs = np.empty(n, np.int8)
+    d = np.empty(n // 32, np.float32)
+    s = np.empty(n // 32, np.float32)
+    lib().orc_q8act_quantize(_p(x), n, _p(qs), _p(d), _p(s))
+    return qs, d, s
+
+
+def block_idots(ty, w, qs):
+    """Per-32-activation-block int32 dots of one weight row against int8 activations."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    qs = np.ascontiguousarray(qs, dtype=np.int8)
+    out = np.empty(qs.size // 32, np.int32)
+    if lib().orc_block_idots(ty, _p(w), _p(qs), qs.size // 32, _p(out)):
+        raise ValueError(f"no block dots for type {ty}")
+    return out
+
+
+def block_idots_rows(ty, w, n_rows, qs):
+    """block_idots of n_rows consecutive rows of w against one int8 activation row: [n_rows, nb32]."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    qs = np.ascontiguousarray(qs, dtype=np.int8)
+    nb = qs.size // 32
+    out = np.empty((n_rows, nb), np.int32)
+    if lib().orc_block_idots_rows(ty, _p(w), n_rows, _p(qs), nb, _p(out)):
+        raise ValueError(f"no block dots for type {ty}")
+    return out
+
+
+def dot(ty, w, x, level=AUTO):
+    """quant::dot of one weight row against f32 activations x (quantised here when needed)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if ty in (F32, F16, BF16):
+        return lib().orc_dot(ty, _p(w), _p(x), None, None, None, x.size, level)
+    qs, d, s = q8act(x)
+    return lib().orc_dot(ty, _p(w), _p(x), _p(qs), _p(d), _p(s), x.size, level)
+
+
+def dot_q(ty, w, qs, d, s, level=AUTO):
+    """quant::dot with given Q8 activations."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    return lib().orc_dot(ty, _p(w), None, _p(qs), _p(d), _p(s), qs.size, level)
+
+
+def dot_f32(a, b, level=AUTO):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return lib().orc_dot_f32(_p(a), _p(b), a.size, level)
+
+
+def axpy(y, a, x, level=AUTO):
+    y = np.array(y, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    lib().orc_axpy(_p(y), a, _p(x), y.size, level)
+    return y
+
+
+def matmul(ty, w, cols, rows, x, threads=1, level=AUTO):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.size // cols
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    out = np.empty((n, rows), np.float32)
+    if lib().orc_matmul(ty, _p(w), cols, rows, _p(x), n, _p(out), threads, level):
+        raise ValueError("orc_matmul failed")
+    return out
+
+
+def softmax(x):
+    x = np.array(x, dtype=np.float32)
+    lib().orc_softmax(_p(x), x.size)
+    return x
+
+
+def sigmoid(x):
+    return lib().orc_sigmoid(x)
+
+
+def silu(x):
+    return lib().orc_silu(x)
+
+
+def rms_norm(x, w, eps, level=AUTO):
+    x = np.array(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    lib().orc_rms_norm(_p(x), _p(w), x.size // w.size, w.size, eps, level)
+    return x
+
+
+def route(logits, k):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    ids = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    lib().orc_route(_p(logits), logits.size, k, _p(ids), _p(w))
+    return ids, w
+
+
+def dense_ffn(gty, gate, uty, up, dty, down, e, ff, x, threads=1, level=AUTO):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.size // e
+    out = np.empty((n, e), np.float32)
+    for a in (gate, up, down):
+        assert a.dtype == np.uint8 and a.flags.c_contiguous
+    if lib().orc_dense_ffn(gty, _p(gate), uty, _p(up), dty, _p(down), e, ff, _p(x), n, _p(out), threads, level):
+        raise ValueError("orc_dense_ffn failed")
+    return out
+
+
+def moe(layer, h, threads=1, level=AUTO, taps=False):
+    """Model::moe of the tokens h [T x E] for a layer made by biv_amd.synth.
+
+    Returns out [T x E] f32 (the block's output, before the residual add), and
+    with taps=True also (ids [T x k], weights [T x k], logits [T x n_expert]).
+    """
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    e, ne, k, ff = layer.n_embd, layer.n_expert, layer.k, layer.n_ff
+    n = h.size // e
+    m = OrcMoe()
+    m.n_expert, m.k, m.n_embd, m.n_ff = ne, k, e, ff
+    m.n_ff_sh = layer.n_ff_sh if layer.shared is not None else 0
+    m.router = OrcWeight(layer.router.ty, 0, _p(layer.router.data))
+    for name in ("gate", "up", "down"):
+        ex = getattr(layer, name)
+        setattr(m, name, OrcExperts(ex.ty, 0, _p(ex.data), ex.stride, ex.offset))
+    if layer.shared is not None:
+        sg, su, sd, gi = layer.shared
+        m.sh_gate = OrcWeight(sg.ty, 0, _p(sg.data))
+        m.sh_up = OrcWeight(su.ty, 0, _p(su.data))
+        m.sh_down = OrcWeight(sd.ty, 0, _p(sd.data))
+        m.gate_inp = OrcWeight(gi.ty, 0, _p(gi.data))
+    out = np.empty((n, e), np.float32)
+    ids = np.empty((n, k), np.int32)
+    w = np.empty((n, k), np.float32)
+    logits = np.empty((n, ne), np.float32)
+    if lib().orc_moe(ctypes.byref(m), _p(h), n, _p(out), threads, level, _p(ids), _p(w), _p(logits)):
+        raise ValueError("orc_moe failed")
+    if taps:
+        return out, ids, w, logits
+    return out

@@ -1,0 +1,208 @@
+"""Parity of the gfx950 MoE block (through the C ABI) with the CPU oracle.
+
+The bar, per forward on the same seeded inputs:
+  - router logits bit-identical (the GPU sums them in the reference's AVX2 order)
+  - top-k expert ids identical, weights within 1e-5 relative
+  - every per-32-block int32 dot of gate, up and down bit-identical to the
+    oracle's integer dot of the same weight row and int8 activations
+  - block output within max|d| <= 1e-3 * RMS(output)
+  - bit-identical from run to run, and a token's output independent of the
+    other tokens in its batch
+"""
+import numpy as np
+import pytest
+
+from biv_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4K, Q6K = synth.Q8_0, synth.Q4K, synth.Q6K
+TOL = 1e-3  # max|d| <= TOL * RMS(reference output)
+
+
+@pytest.fixture(scope="module")
+def engine():
+    from biv_amd import hip
+    e = hip.HipEngine(0)
+    yield e
+    e.close()
+
+
+_layers = {}
+
+
+def layer_for(engine, **kw):
+    key = tuple(sorted(kw.items()))
+    if key not in _layers:
+        layer = synth.make_layer(**kw)
+        _layers[key] = (layer, engine.moe(layer))
+    return _layers[key]
+
+
+def check_output(ref, got, tol=TOL):
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    err = float(np.abs(ref.astype(np.float64) - got).max())
+    assert err <= tol * rms, f"max|d| {err:.3e} > {tol} * RMS {rms:.3e}"
+    return err / rms
+
+
+def check_block_dots(orc, layer, h, t):
+    """gate/up/down int32 block dots of every pair (and shared row) against
+    the oracle's, on the same int8 activations."""
+    T, k, E, ff = h.shape[0], layer.k, layer.n_embd, layer.n_ff
+    P = T * k
+    xq = [orc.q8act(h[i])[0] for i in range(T)]
+    for p in range(P + (T if layer.shared is not None else 0)):
+        if p < P:
+            e, tok = int(t["pair_expert"][p]), int(t["pair_token"][p])
+            gw, uw, dw = layer.gate.expert(e), layer.up.expert(e), layer.down.expert(e)
+            gty, uty, dty = layer.gate.ty, layer.up.ty, layer.down.ty
+        else:
+            tok = p - P
+            sg, su, sd, _ = layer.shared
+            gw, uw, dw, gty, uty, dty = sg.data, su.data, sd.data, sg.ty, su.ty, sd.ty
+        assert np.array_equal(t["gate_idots"][p], orc.block_idots_rows(gty, gw, ff, xq[tok])), ("gate", p)
+        assert np.array_equal(t["up_idots"][p], orc.block_idots_rows(uty, uw, ff, xq[tok])), ("up", p)
+        assert np.array_equal(t["down_idots"][p], orc.block_idots_rows(dty, dw, E, t["act_q"][p])), ("down", p)
+
+
+def check_dispatch(t, ids, T, k):
+    """Dispatch order: pairs grouped by ascending expert, tokens ascending
+    within an expert, exactly the pairs the routing chose."""
+    pe, pt = t["pair_expert"], t["pair_token"]
+    order = np.lexsort((pt, pe))
+    assert np.array_equal(order, np.arange(T * k))
+    want = sorted((int(ids[tok, j]), tok) for tok in range(T) for j in range(k))
+    assert [(int(a), int(b)) for a, b in zip(pe, pt)] == want
+
+
+def check_act(orc, layer, h, t):
+    """The quantised SwiGLU intermediate: the GPU's f32 sums differ from the
+    CPU's only in rounding, so its int8 is within 1 of the oracle's."""
+    T, k, E, ff = h.shape[0], layer.k, layer.n_embd, layer.n_ff
+    for p in range(T * k):
+        e, tok = int(t["pair_expert"][p]), int(t["pair_token"][p])
+        g = orc.matmul(layer.gate.ty, layer.gate.expert(e), E, ff, h[tok])
+        u = orc.matmul(layer.up.ty, layer.up.expert(e), E, ff, h[tok])
+        a = np.array([orc.silu(float(x)) for x in g[0]], np.float32) * u[0]
+        q, d, _ = orc.q8act(a.astype(np.float32))
+        diff = np.abs(q.astype(np.int32) - t["act_q"][p].astype(np.int32))
+        assert diff.max() <= 1, (p, diff.max())
+        assert np.allclose(d, t["act_d"][p], rtol=1e-4)
+
+
+def full_parity(orc, engine, layer, moe, h, block_dots=True):
+    T = h.shape[0]
+    ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
+    got, t = moe.ffn_taps(h)
+    if orc.detect_level() >= orc.AVX2:
+        assert np.array_equal(t["logits"].view(np.uint32), logits.view(np.uint32)), "router logits differ"
+    assert np.array_equal(t["ids"], ids), "top-k ids differ"
+    assert np.allclose(t["weights"], w, rtol=1e-5, atol=1e-7)
+    check_dispatch(t, ids, T, layer.k)
+    if block_dots:
+        check_block_dots(orc, layer, h, t)
+    rel = check_output(ref, got)
+    again = moe.ffn(h)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "not bit-identical run to run"
+    return rel, t
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 9])
+def test_q8_small_layer(orc, engine, T):
+    print(f"case q8 small T={T}", flush=True)
+    layer, moe = layer_for(engine, seed=21, n_expert=32)
+    h = synth.make_tokens(100 + T, T, offsets=True)
+    full_parity(orc, engine, layer, moe, h)
+
+
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_q8_full_layer_decode(orc, engine, T):
+    """The named decode configs: 256 experts, E=2048, ff=512, k=8, T=1/5/40."""
+    print(f"case q8 full T={T}", flush=True)
+    layer, moe = layer_for(engine, seed=1)
+    h = synth.make_tokens(200 + T, T, offsets=T > 1)
+    rel, t = full_parity(orc, engine, layer, moe, h, block_dots=T <= 5)
+    if T <= 5:
+        check_act(orc, layer, h, t)
+
+
+@pytest.mark.parametrize("skew", [0.13, 1.0])
+def test_q8_prefill_zipf_512(orc, engine, skew):
+    """T=512 with Zipf-skewed routing (config 3): skew 0.13 puts ~60 tokens on
+    the hottest expert; 1.0 leaves most experts idle and ~500 on the hottest."""
+    print(f"case q8 zipf T=512 skew={skew}", flush=True)
+    layer, moe = layer_for(engine, seed=1)
+    h = synth.zipf_bias_tokens(layer, 3, 512, scale=skew)
+    ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
+    got, t = moe.ffn_taps(h, dots=False)
+    assert np.array_equal(t["ids"], ids)
+    check_dispatch(t, ids, 512, layer.k)
+    check_output(ref, got)
+    again = moe.ffn(h)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
+def test_kquant_layer(orc, engine):
+    """Q4_K gate/up, Q6_K down (config 4) at small expert count."""
+    print("case kquant", flush=True)
+    layer, moe = layer_for(engine, seed=31, n_expert=32, types=(Q4K, Q4K, Q6K))
+    for T in (1, 6):
+        h = synth.make_tokens(300 + T, T, offsets=True)
+        full_parity(orc, engine, layer, moe, h)
+
+
+def test_mixed_shared_types(orc, engine):
+    """A shared expert in Q8_0 beside Q4_K/Q6_K experts runs in its own launch."""
+    print("case mixed shared", flush=True)
+    layer, moe = layer_for(engine, seed=41, n_expert=16, types=(Q4K, Q4K, Q6K), shared_types=(Q8_0, Q8_0, Q8_0))
+    h = synth.make_tokens(7, 3)
+    full_parity(orc, engine, layer, moe, h)
+
+
+def test_fused_gate_up_offset(orc, engine):
+    """ffn_gate_up_exps: gate and up share one tensor, up at an offset (model.rs:389-399)."""
+    print("case fused gate_up", flush=True)
+    layer, moe = layer_for(engine, seed=51, n_expert=16, fused_gate_up=True)
+    assert layer.up.offset > 0
+    h = synth.make_tokens(8, 4)
+    full_parity(orc, engine, layer, moe, h)
+
+
+def test_no_shared_expert_and_add(orc, engine):
+    print("case no shared / add", flush=True)
+    layer, moe = layer_for(engine, seed=61, n_expert=16, k=4, shared=False)
+    h = synth.make_tokens(9, 3)
+    full_parity(orc, engine, layer, moe, h)
+    x = synth.make_tokens(10, 3)
+    ref = orc.moe(layer, h)
+    got = moe.ffn(h, out=x.copy(), add=True)
+    check_output(ref, got - x, tol=2 * TOL)
+    assert np.array_equal(got.view(np.uint32), (x + moe.ffn(h)).view(np.uint32))
+
+
+def test_batch_independence(orc, engine):
+    """A token's output does not depend on the other tokens in its pass (the
+    bit-identical batched-vs-alone property of biv's batch examples)."""
+    print("case batch independence", flush=True)
+    layer, moe = layer_for(engine, seed=21, n_expert=32)
+    h = synth.make_tokens(11, 6, offsets=True)
+    batched = moe.ffn(h)
+    for i in range(6):
+        alone = moe.ffn(h[i:i + 1])
+        assert np.array_equal(alone[0].view(np.uint32), batched[i].view(np.uint32)), i
+
+
+def test_empty_and_errors(engine):
+    from biv_amd import hip
+    layer, moe = layer_for(engine, seed=21, n_expert=32)
+    out = moe.ffn(np.zeros((0, 2048), np.float32))
+    assert out.shape == (0, 2048)
+    bad = synth.Experts(1, 2048, 512, 2, np.zeros(2 * 512 * 4096, np.uint8), 512 * 4096)
+    x = engine.upload_experts(bad)  # F16 uploads, but has no expert kernel
+    with pytest.raises(hip.HipError) as e:
+        import ctypes
+        o = ctypes.c_void_p()
+        engine._check(engine.L.biv_hip_moe_create(engine.h, engine.upload_weight(layer.router), x, x, x,
+                                                  None, None, None, None, 8, ctypes.byref(o)))
+    assert e.value.code == -2
