@@ -23,6 +23,10 @@ __device__ inline float f16_at(const uint8_t *p)
 
 __device__ inline int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// e^x rounded once from double: the nearest float, which is what glibc's
+// expf (the f32::exp of the reference on Linux) returns
+__device__ inline float exp_f32(float x) { return (float)exp((double)x); }
+
 // byte i (0..15) of a 16-byte vector, without indexing a private array
 __device__ inline int byte_at(const int4 &v, int i)
 {
@@ -147,9 +151,7 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
 #pragma unroll
     for (int j = 0; j < PER; j++) {
         int i = lane + WAVE * j;
-        // exp of the f32 difference, rounded once from double: the nearest
-        // float to e^x, which is what glibc's expf returns
-        v[j] = i < n_expert ? (float)exp((double)(v[j] - mx)) : 0.0f;
+        v[j] = i < n_expert ? exp_f32(v[j] - mx) : 0.0f;
         sum += v[j];
     }
 #pragma unroll
@@ -342,6 +344,16 @@ template <> struct WBlock<T_Q8_0> {
         idot = acc;
         return (float)acc * (d * x.d);
     }
+    // The eight 4-byte partial sums the reference's 8 i32 lanes hold, and the
+    // block's f32 scale f16(d) * x.d (quant.rs:1373-1378).
+    __device__ inline void partials(const XBlock &x, int v[8], float &c, float &mt, float &dm) const
+    {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = dot4(q[i], x.v[i], 0);
+        c = d * x.d;
+        mt = 0.0f;
+        dm = 0.0f;
+    }
 };
 
 // q4_K: sub-block sb of a 256-element super-block; 6-bit scale and min from
@@ -374,7 +386,11 @@ template <> struct WBlock<T_Q4K> {
         }
         dsc = d * (float)s;
         dmn = dmin * (float)m;
+        dmin_ = dmin;
+        m_ = m;
     }
+    float dmin_;
+    int m_;
     __device__ inline float dot(const XBlock &x, int &idot) const
     {
         int acc = 0;
@@ -382,6 +398,16 @@ template <> struct WBlock<T_Q4K> {
         for (int i = 0; i < 8; i++) acc = dot4(q[i], x.v[i], acc);
         idot = acc;
         return (float)acc * (dsc * x.d) - dmn * x.s;
+    }
+    // lanes of dot_u8_i8(nibbles, x), scale d*sc*x.d, and the min term m*x.s
+    // with the super-block's dmin (quant.rs:1394-1420)
+    __device__ inline void partials(const XBlock &x, int v[8], float &c, float &mt, float &dm) const
+    {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = dot4(q[i], x.v[i], 0);
+        c = dsc * x.d;
+        mt = (float)m_ * x.s;
+        dm = dmin_;
     }
 };
 
@@ -426,12 +452,26 @@ template <> struct WBlock<T_Q6K> {
         idot = isum;
         return (float)isum * (d * x.d);
     }
+    // lanes of madd(maddubs(q, x) - maddubs(32, x), sc): lanes 0-3 carry
+    // elements 0..15 under sc0, lanes 4-7 elements 16..31 under sc1
+    // (quant.rs:1510-1527)
+    __device__ inline void partials(const XBlock &x, int v[8], float &c, float &mt, float &dm) const
+    {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            v[i] = (i < 4 ? sc0 : sc1) * (dot4(q[i], x.v[i], 0) - 32 * dot4(0x01010101, x.v[i], 0));
+        c = d * x.d;
+        mt = 0.0f;
+        dm = 0.0f;
+    }
 };
+
+__device__ inline float sigmoid(float x) { return 1.0f / (1.0f + exp_f32(-x)); }
 
 __device__ inline float silu_mul(float g, float u)
 {
     // ops::silu(g) * u (ops.rs:159-167, model.rs:1121-1124)
-    return (g * (1.0f / (1.0f + expf(-g)))) * u;
+    return (g * sigmoid(g)) * u;
 }
 
 // ---------------------------------------------------------------------------
@@ -510,6 +550,131 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_expert_mv(MvArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// Gate/up in the reference's f32 order.  The SwiGLU intermediate is quantised
+// again before the down projection, so any difference in the rounding of
+// gate or up can move an int8 of the intermediate by one.  These sums are
+// therefore formed exactly as biv's x86 kernels form them (quant.rs:1368-1533):
+// every block gives eight 4-byte i32 partials (the 8 lanes of a ymm
+// register), converted to f32 and FMA'd with the block's scale into one of two
+// accumulators by block parity; then acc0 + acc1 and the hsum tree
+// (quant.rs:1149-1153); for Q4_K the mins are summed apart and subtracted
+// last.  The result is the reference's f32, bit for bit.
+//
+// A wave first stores the partials of 4 (matrix, row, token) combinations in
+// LDS ("fills"), then 16 lanes per combination run the 16 FMA chains.
+constexpr int GU_TCH = 2; // tokens per chunk
+constexpr int SLOT = 11;  // floats per block in LDS: 8 partials, scale, min term, dmin
+
+template <int TY, int G, bool DUMP>
+__global__ __launch_bounds__(MV_WAVES *WAVE) void k_gateup_exact(MvArgs a)
+{
+    constexpr int RPW = WAVE / G;          // rows per wave
+    constexpr int FILLS = 4 / RPW;         // fills per chain pass
+    constexpr int COMBOS = 2 * RPW * GU_TCH; // per token chunk: (gate, up) x rows x tokens
+    constexpr int PASSES = COMBOS / 4;
+    __shared__ float sp[MV_WAVES][4][G][SLOT];
+    __shared__ float sr[MV_WAVES][COMBOS];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int b = lane % G, rg = lane / G;
+    const int u = blockIdx.y;
+    const bool shared = u == a.u_max;
+    int e = 0, beg, cnt;
+    if (shared) {
+        beg = a.P;
+        cnt = a.T;
+    } else {
+        if (u >= *a.dp.n_active) return; // uniform over the workgroup
+        e = a.dp.act_expert[u];
+        beg = a.dp.act_beg[u];
+        cnt = a.dp.act_cnt[u];
+    }
+    const DevMat &A = shared ? a.sa : a.a;
+    const DevMat &B = shared ? a.sb : a.b;
+    const int rows = A.rows, K = A.cols;
+    const int row0 = (blockIdx.x * MV_WAVES + wave) * RPW;
+    const int row = row0 + rg;
+    const bool row_ok = row < rows;
+    const size_t mrow = (size_t)e * rows + (row_ok ? row : 0);
+    WBlock<TY> wm[2];
+    wm[0].load(A, mrow, b);
+    wm[1].load(B, mrow, b);
+    // chain lane roles: combination cb, parity pi, ymm lane l
+    const int cb = lane >> 4, pi = (lane >> 3) & 1, l = lane & 7;
+    for (int i0 = 0; i0 < cnt; i0 += GU_TCH) {
+        for (int pass = 0; pass < PASSES; pass++) {
+#pragma unroll
+            for (int f = 0; f < FILLS; f++) {
+                const int slot = f * RPW + rg;          // 0..3 within the pass
+                const int idx = (pass * 4 + f * RPW) / RPW; // (matrix, token) index
+                const int m = idx & 1, j = idx >> 1;
+                const int i = i0 + j;
+                float *dst = sp[wave][slot][b];
+                if (i < cnt && row_ok) {
+                    const size_t xrow = shared ? (size_t)i : (size_t)a.dp.pair_tok[beg + i];
+                    XBlock x;
+                    load_x(a.xq, a.xd, a.xs, xrow, K, b, x);
+                    int v[8];
+                    float c, mt, dm;
+                    if (m == 0) wm[0].partials(x, v, c, mt, dm);
+                    else wm[1].partials(x, v, c, mt, dm);
+#pragma unroll
+                    for (int q = 0; q < 8; q++) dst[q] = (float)v[q];
+                    dst[8] = c;
+                    dst[9] = mt;
+                    dst[10] = dm;
+                    if (DUMP) {
+                        int32_t *dump = m == 0 ? a.dump_a : a.dump_b;
+                        if (dump) {
+                            int sum = 0;
+#pragma unroll
+                            for (int q = 0; q < 8; q++) sum += v[q];
+                            dump[((size_t)(beg + i) * rows + row) * G + b] = sum;
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < SLOT; q++) dst[q] = 0.0f;
+                }
+            }
+            __syncthreads();
+            // 16 chains per combination: acc over blocks pi, pi+2, ... in order
+            const float(*blk)[SLOT] = sp[wave][cb];
+            float acc = 0.0f;
+#pragma unroll 8
+            for (int s2 = 0; s2 < G / 2; s2++) {
+                const int bb = 2 * s2 + pi;
+                acc = fmaf(blk[bb][l], blk[bb][8], acc);
+            }
+            float t = acc + __shfl_xor(acc, 8); // acc0 + acc1
+            t = t + __shfl_xor(t, 4);           // 128-bit halves
+            t = t + __shfl_xor(t, 2);           // movehl
+            t = t + __shfl_xor(t, 1);           // movehdup
+            if (TY == T_Q4K && (lane & 15) == 0) {
+                // mins += dmin * (m1 * s[2j] + m2 * s[2j+1]), in block order
+                float mins = 0.0f;
+                for (int s2 = 0; s2 < G / 2; s2++)
+                    mins = mins + blk[2 * s2][10] * (blk[2 * s2][9] + blk[2 * s2 + 1][9]);
+                t = t - mins;
+            }
+            if ((lane & 15) == 0) sr[wave][pass * 4 + cb] = t;
+            __syncthreads();
+        }
+        // combination index c = (j * 2 + m) * RPW + rg
+        if (b == 0 && row_ok) {
+#pragma unroll
+            for (int j = 0; j < GU_TCH; j++) {
+                const int i = i0 + j;
+                if (i >= cnt) break;
+                const float g = sr[wave][(j * 2 + 0) * RPW + rg];
+                const float up = sr[wave][(j * 2 + 1) * RPW + rg];
+                a.out[(size_t)(beg + i) * rows + row] = silu_mul(g, up);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Combine (model.rs:884-896): out[t] = 0; for each of t's experts in
 // ascending id, out = fma(w, y, out) (quant::axpy, quant.rs:1209-1226); then
 // out = fma(sigmoid(g), y_shared, out).  Then out is written or added.
@@ -527,7 +692,7 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, Di
     }
     if (has_shared) {
         float g = glogit[t];
-        float sg = 1.0f / (1.0f + expf(-g));
+        float sg = sigmoid(g);
         o = fmaf(sg, y[(size_t)(P + t) * E + c], o);
     }
     float *po = out + (size_t)t * E + c;
@@ -561,6 +726,36 @@ hipError_t launch_mv_t(MvArgs a, int routed, int shared, hipStream_t st)
     BIV_MV_CASE(T_Q6K, 32)
     BIV_MV_CASE(T_Q6K, 16)
 #undef BIV_MV_CASE
+    return hipErrorInvalidValue;
+}
+
+// One launch of the exact gate/up kernel over routed slots and/or the shared expert.
+template <bool DUMP>
+hipError_t launch_gu_t(MvArgs a, int routed, int shared, hipStream_t st)
+{
+    const DevMat &M = routed ? a.a : a.sa;
+    const int G = M.cols / 32;
+    if (!routed) a.u_max = 0;
+    const int slots = (routed ? a.u_max : 0) + (shared ? 1 : 0);
+    if (slots == 0) return hipSuccess;
+    const int rows_per_wg = MV_WAVES * (WAVE / G);
+    dim3 grid((M.rows + rows_per_wg - 1) / rows_per_wg, slots);
+    dim3 block(MV_WAVES * WAVE);
+#define BIV_GU_CASE(TY, GG)                                                                                     \
+    if (M.ty == TY && G == GG) {                                                                                \
+        k_gateup_exact<TY, GG, DUMP><<<grid, block, 0, st>>>(a);                                                \
+        return hipGetLastError();                                                                               \
+    }
+    BIV_GU_CASE(T_Q8_0, 64)
+    BIV_GU_CASE(T_Q8_0, 32)
+    BIV_GU_CASE(T_Q8_0, 16)
+    BIV_GU_CASE(T_Q4K, 64)
+    BIV_GU_CASE(T_Q4K, 32)
+    BIV_GU_CASE(T_Q4K, 16)
+    BIV_GU_CASE(T_Q6K, 64)
+    BIV_GU_CASE(T_Q6K, 32)
+    BIV_GU_CASE(T_Q6K, 16)
+#undef BIV_GU_CASE
     return hipErrorInvalidValue;
 }
 
@@ -618,7 +813,16 @@ hipError_t launch_sort(const int *ids, const float *wts, int n_expert, int k, in
     return hipGetLastError();
 }
 
-hipError_t launch_gateup(const MvArgs &a, hipStream_t st) { return launch_mv<true>(a, st); }
+hipError_t launch_gateup(const MvArgs &a, hipStream_t st)
+{
+    const bool dump = a.dump_a || a.dump_b;
+    const bool has_shared = a.sa.q != nullptr;
+    const bool together = has_shared && a.sa.ty == a.a.ty && a.sa.cols == a.a.cols && a.sa.rows == a.a.rows;
+    if (together) return dump ? launch_gu_t<true>(a, 1, 1, st) : launch_gu_t<false>(a, 1, 1, st);
+    hipError_t err = dump ? launch_gu_t<true>(a, 1, 0, st) : launch_gu_t<false>(a, 1, 0, st);
+    if (err != hipSuccess || !has_shared) return err;
+    return dump ? launch_gu_t<true>(a, 0, 1, st) : launch_gu_t<false>(a, 0, 1, st);
+}
 
 hipError_t launch_down(const MvArgs &a, hipStream_t st) { return launch_mv<false>(a, st); }
 
