@@ -1,0 +1,206 @@
+#!/usr/bin/env python3
+"""Throughput of the qwen35moe MoE FFN block on one MI355X.
+
+A step is one forward of one MoE layer (router, routing, dispatch, grouped
+Q8_0 expert SwiGLU, shared expert, combine) over T tokens already resident in
+HBM.  The headline workload is the decode-verify configuration (T = 5: one
+token plus four MTP drafts); T = 1, 40 and the
+T = 512 Zipf-skewed prefill chunk are reported in `sweep`.
+
+Steps rotate over `--layers` distinct copies of the layer in HBM (16 x 856 MB
+by default), so the expert weights a step reads are not left in the 256 MB
+Infinity Cache by the step before: the figure is HBM-honest.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+E, NE, K, FF = 2048, 256, 8, 512
+Q8_ROW_E = 2048 // 32 * 34   # bytes of a Q8_0 row of 2048
+Q8_ROW_FF = 512 // 32 * 34   # bytes of a Q8_0 row of 512
+EXPERT_BYTES = 2 * FF * Q8_ROW_E + E * Q8_ROW_FF   # 3,342,336
+ROUTER_BYTES = NE * E * 4 + E * 4                  # router + gate_inp (f32)
+HBM_PEAK = 8.0e12
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def layer_bytes(U, T):
+    """Algorithmic HBM bytes of one layer: the U routed experts and the shared
+    expert (read once each), the router and gate_inp, h in and out out."""
+    return (U + 1) * EXPERT_BYTES + ROUTER_BYTES + 2 * T * E * 4
+
+
+def stage_bytes(stage, U, T):
+    """Algorithmic bytes of one stage's launch (weights read once, activations
+    read and written once)."""
+    P = T * K
+    R = P + T
+    if stage == "gate_up":
+        return (U + 1) * 2 * FF * Q8_ROW_E + T * E * 9 // 8 + R * FF * 4
+    if stage == "down":
+        return (U + 1) * E * Q8_ROW_FF + R * FF * 9 // 8 + R * E * 4
+    if stage == "router":
+        return ROUTER_BYTES + T * E * 4 + T * (NE + 1) * 4
+    if stage == "combine":
+        return R * E * 4 + T * E * 4 + P * 8
+    if stage == "quant_h":
+        return T * E * 4 + T * E * 9 // 8
+    if stage == "quant_act":
+        return R * FF * 4 + R * FF * 9 // 8
+    return 0
+
+
+def tokens_for(layer, T, seed):
+    from biv_amd import synth
+    if T >= 512:
+        return synth.zipf_bias_tokens(layer, seed, T)
+    return synth.make_tokens(seed, T, offsets=T > 1)
+
+
+def bench_gpu(eng, moes, layer, T, steps, warmup, torch):
+    import numpy as np
+    h = tokens_for(layer, T, 1000 + T)
+    _, taps = moes[0].ffn_taps(h, dots=False)
+    U = int(np.unique(taps["ids"]).size)
+    h_dev = torch.from_numpy(h).cuda()
+    out_dev = torch.empty_like(h_dev)
+    L = len(moes)
+    for i in range(warmup):
+        moes[i % L].forward_device(h_dev.data_ptr(), T, out_dev.data_ptr())
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall = time.perf_counter()
+    t0.record()
+    for i in range(steps):
+        moes[i % L].forward_device(h_dev.data_ptr(), T, out_dev.data_ptr())
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall
+    ms = t0.elapsed_time(t1) / steps
+    # a second timed region with an event around every stage, for the
+    # per-kernel roofline (events add small gaps, so not the headline)
+    eng.set_timing(True)
+    for i in range(steps):
+        moes[i % L].forward_device(h_dev.data_ptr(), T, out_dev.data_ptr())
+    stage_ms, n = eng.stage_times()
+    eng.set_timing(False)
+    stage_us = {k: 1e3 * v / n for k, v in stage_ms.items()}
+    B = layer_bytes(U, T)
+    res = {
+        "T": T, "U": U, "us_per_layer": round(ms * 1e3, 3), "tokens_per_s": round(T / (ms * 1e-3), 1),
+        "layer_GBps": round(B / (ms * 1e-3) / 1e9, 1), "layer_hbm_frac": round(B / (ms * 1e-3) / HBM_PEAK, 4),
+        "stage_us": {k: round(v, 3) for k, v in stage_us.items()},
+        "wall_s": round(wall, 3),
+    }
+    dom = max(("gate_up", "down", "router"), key=lambda s: stage_us[s])
+    dbytes = stage_bytes(dom, U, T)
+    ach = dbytes / (stage_us[dom] * 1e-6) / 1e9
+    res["roofline"] = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK / 1e9,
+                       "unit": "GB/s", "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": None,
+                       "bytes_per_launch": dbytes, "avg_us": round(stage_us[dom], 3)}
+    return res
+
+
+def bench_cpu(layer, T, seconds):
+    """The oracle (C restatement of biv's AVX2/AVX-VNNI CPU path) on the host cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    if not os.path.exists(oracle.LIB_PATH):
+        oracle.build()
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
+    h = tokens_for(layer, T, 1000 + T)
+    oracle.moe(layer, h, threads=threads)  # warm
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        oracle.moe(layer, h, threads=threads)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    level = {0: "scalar", 1: "avx2", 2: "avxvnni"}[oracle.detect_level()]
+    return {"value": round(T / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "us_per_layer": round(dt * 1e6, 1), "kernels": level,
+            "sample": f"{n} forwards of the same T={T} Q8_0 layer ({seconds:.0f} s budget)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=16, help="distinct layer copies rotated in HBM")
+    ap.add_argument("--T", type=int, default=5, help="tokens per step of the headline workload")
+    ap.add_argument("--sweep", default="1,40,512", help="other T values to report ('' for none)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 to skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from biv_amd import hip, synth
+    t = time.perf_counter()
+    layer = synth.make_layer(1)
+    log(f"layer generated in {time.perf_counter() - t:.1f}s")
+    eng = hip.HipEngine(0)
+    # one default-priority stream for the library's kernels and the timing events
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    eng.set_stream(stream.cuda_stream)
+    t = time.perf_counter()
+    moes = [eng.moe(layer) for _ in range(args.layers)]
+    log(f"{args.layers} layer copies uploaded ({eng.device_bytes() / 1e9:.1f} GB) in {time.perf_counter() - t:.1f}s")
+
+    main_res = bench_gpu(eng, moes, layer, args.T, args.steps, args.warmup, torch)
+    log(f"T={args.T}: {main_res}")
+    sweep = {}
+    for T in [int(x) for x in args.sweep.split(",") if x.strip()]:
+        steps = args.steps if T <= 64 else max(20, args.steps // 4)
+        sweep[str(T)] = bench_gpu(eng, moes, layer, T, steps, args.warmup, torch)
+        log(f"T={T}: {sweep[str(T)]}")
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = bench_cpu(layer, args.T, args.cpu_seconds)
+        log(f"cpu: {cpu}")
+
+    ms = main_res["us_per_layer"] / 1e3
+    line = {
+        "metric": "MoE-layer tokens/s (qwen35moe, Q8_0, T=5 decode-verify)",
+        "value": main_res["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_layer": main_res["us_per_layer"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,0.02) weights quantised to Q8_0, N(0,1) tokens)",
+        "config": {"workload": "qwen35moe MoE FFN layer, Q8_0, decode-verify T=5 (configs[1])",
+                   "n_embd": E, "n_expert": NE, "k": K, "n_ff": FF, "n_ff_shared": FF, "T": args.T,
+                   "distinct_experts_U": main_res["U"], "layers_rotated": args.layers},
+        "roofline": main_res["roofline"],
+        "layer_roofline": {"bound": "hbm", "achieved": main_res["layer_GBps"], "peak": HBM_PEAK / 1e9,
+                           "unit": "GB/s", "frac": main_res["layer_hbm_frac"]},
+        "stage_us": main_res["stage_us"],
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+    eng.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -3,6 +3,7 @@
 // queues the kernels of kernels.hip on the context's stream.
 #include "../../include/biv_hip.h"
 #include "common.hpp"
+#include "layout.hpp"
 
 #include <algorithm>
 #include <cstdarg>
@@ -61,6 +62,11 @@ struct biv_hip_ctx {
     Scratch sc;
     // scratch shape: the widest layer seen
     int sc_E = 0, sc_ff = 0, sc_ne = 0, sc_k = 0;
+    // stage timing (biv_hip_set_timing): one event before each stage and
+    // one after the last, per forward, read back by biv_hip_stage_times
+    bool timing = false;
+    std::vector<hipEvent_t> ev_pool;
+    std::vector<std::vector<hipEvent_t>> ev_fwd;
 };
 
 namespace {
@@ -139,33 +145,65 @@ int upload_mat(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, con
     case BIV_GGML_Q6_K: qrow = cols / 256 * 192; srow = cols / 256 * 16; drow = cols / 256 * 2; break;
     default: qrow = row_bytes; break;
     }
+    // the chain layouts (layout.hpp) need whole groups of blocks per row
+    if ((ty == BIV_GGML_Q8_0 || ty == BIV_GGML_Q4_K) && cols % 256)
+        return fail(ctx, BIV_HIP_E_INVALID, "width %zu: Q8_0/Q4_K rows must be a multiple of 256", cols);
+    if (ty == BIV_GGML_Q6_K && cols % 512)
+        return fail(ctx, BIV_HIP_E_INVALID, "width %zu: Q6_K rows must be a multiple of 512", cols);
+    if (ty == BIV_GGML_F32 && cols % 128)
+        return fail(ctx, BIV_HIP_E_INVALID, "width %zu: F32 rows must be a multiple of 128", cols);
+    const int K = (int)cols;
     std::vector<uint8_t> q(nr * qrow), s(nr * srow), d(nr * drow);
     for (size_t e = 0; e < n; e++)
         for (size_t r = 0; r < rows; r++) {
             const uint8_t *src = src_row(e, r);
             const size_t i = e * rows + r;
+            uint8_t *qd = &q[i * qrow], *sd = srow ? &s[i * srow] : nullptr, *dd = drow ? &d[i * drow] : nullptr;
             switch (ty) {
             case BIV_GGML_Q8_0:
-                for (size_t b = 0; b < cols / 32; b++) {
-                    memcpy(&s[i * srow + 2 * b], src + 34 * b, 2);
-                    memcpy(&q[i * qrow + 32 * b], src + 34 * b + 2, 32);
+                for (int b = 0; b < K / 32; b++) {
+                    const uint8_t *blk = src + 34 * b;
+                    memcpy(sd + 2 * biv::lay::q8_scale(K, b), blk, 2);
+                    for (int l = 0; l < 8; l++) memcpy(qd + 4 * biv::lay::q8_word(b, l), blk + 2 + 4 * l, 4);
                 }
                 break;
             case BIV_GGML_Q4_K:
-                for (size_t b = 0; b < cols / 256; b++) {
-                    memcpy(&s[i * srow + 16 * b], src + 144 * b, 16);
-                    memcpy(&q[i * qrow + 128 * b], src + 144 * b + 16, 128);
+                for (int sb = 0; sb < K / 256; sb++) {
+                    const uint8_t *blk = src + 144 * sb;
+                    memcpy(sd + 16 * sb, blk, 16); // d, dmin, the 12 scale bytes
+                    for (int j = 0; j < 4; j++)
+                        for (int l = 0; l < 8; l++)
+                            memcpy(qd + 4 * biv::lay::q4k_word(4 * sb + j, l), blk + 16 + 32 * j + 4 * l, 4);
                 }
                 break;
-            case BIV_GGML_Q6_K:
-                for (size_t b = 0; b < cols / 256; b++) {
-                    memcpy(&q[i * qrow + 192 * b], src + 210 * b, 192);
-                    memcpy(&s[i * srow + 16 * b], src + 210 * b + 192, 16);
-                    memcpy(&d[i * drow + 2 * b], src + 210 * b + 208, 2);
+            case BIV_GGML_Q6_K: {
+                const int nsb = K / 256;
+                uint8_t *qh = qd + 128 * nsb;
+                for (int sb = 0; sb < nsb; sb++) {
+                    const uint8_t *blk = src + 210 * sb;
+                    for (int h = 0; h < 2; h++) {
+                        const int qq = 2 * sb + h;
+                        for (int l = 0; l < 8; l++) {
+                            for (int pi = 0; pi < 2; pi++)
+                                memcpy(qd + 4 * biv::lay::q6k_ql_word(qq, pi, l), blk + 64 * h + 32 * pi + 4 * l, 4);
+                            memcpy(qh + 4 * biv::lay::q6k_qh_word(qq, l), blk + 128 + 32 * h + 4 * l, 4);
+                        }
+                        // sub-scale sc[8h + 2k + hsel] belongs to chain pi = k & 1 at
+                        // step s = 2 qq + (k >> 1)
+                        for (int k = 0; k < 4; k++)
+                            for (int hsel = 0; hsel < 2; hsel++)
+                                sd[biv::lay::q6k_sc(K, k & 1, hsel, 2 * qq + (k >> 1))] = blk[192 + 8 * h + 2 * k + hsel];
+                    }
+                    memcpy(dd + 2 * sb, blk + 208, 2);
                 }
+                break;
+            }
+            case BIV_GGML_F32:
+                for (int e2 = 0; e2 < K; e2++)
+                    memcpy(qd + 4 * biv::lay::f32_elem(e2 / 32, e2 % 32), src + 4 * e2, 4);
                 break;
             default:
-                memcpy(&q[i * qrow], src, row_bytes);
+                memcpy(qd, src, row_bytes);
                 break;
             }
         }
@@ -251,6 +289,36 @@ struct Dumps {
     int32_t *gate = nullptr, *up = nullptr, *down = nullptr;
 };
 
+constexpr int N_STAGES = 8; // quantise h, router, route, dispatch, gate/up, quantise act, down, combine
+
+// The stage markers of one forward when timing is on.
+struct StageMarks {
+    biv_hip_ctx *ctx;
+    std::vector<hipEvent_t> ev;
+    explicit StageMarks(biv_hip_ctx *c) : ctx(c) {}
+    hipError_t mark()
+    {
+        if (!ctx->timing) return hipSuccess;
+        hipEvent_t e;
+        if (!ctx->ev_pool.empty()) {
+            e = ctx->ev_pool.back();
+            ctx->ev_pool.pop_back();
+        } else {
+            hipError_t err = hipEventCreate(&e);
+            if (err != hipSuccess) return err;
+        }
+        ev.push_back(e);
+        return hipEventRecord(e, ctx->stream);
+    }
+    ~StageMarks()
+    {
+        if (!ctx->timing) return;
+        if (ev.size() == N_STAGES + 1) ctx->ev_fwd.push_back(ev);
+        else
+            for (auto e : ev) ctx->ev_pool.push_back(e);
+    }
+};
+
 // Queue the whole block: h and out are device pointers.
 int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float *out, unsigned flags,
             const Dumps &dm)
@@ -258,19 +326,26 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     if (T == 0) return 0;
     int rc = scratch_fit(ctx, m, T);
     if (rc) return rc;
+    StageMarks mk(ctx);
+#define MARK() HIP_TRY(ctx, mk.mark(), "timing event")
     Scratch &s = ctx->sc;
     hipStream_t st = ctx->stream;
     const int E = m->E, ff = m->ff, ne = m->n_expert, k = m->k;
     const int P = T * k;
     const bool has_shared = m->sg != nullptr;
-    HIP_TRY(ctx, biv::launch_quant_rows(h, T * E / 32, s.xq, s.xd, s.xs, st), "quantise h");
+    MARK();
+    HIP_TRY(ctx, biv::launch_quant_rows(h, T * E / 32, E, s.xq, s.xd, s.xs, st), "quantise h");
+    MARK();
     HIP_TRY(ctx,
             biv::launch_router(reinterpret_cast<const float *>(m->router->m.q),
                                has_shared ? reinterpret_cast<const float *>(m->gi->m.q) : nullptr, ne, E, h, T,
                                s.logits, s.glogit, st),
             "router");
+    MARK();
     HIP_TRY(ctx, biv::launch_route(s.logits, ne, k, T, s.dp.ids, s.dp.wts, st), "route");
+    MARK();
     HIP_TRY(ctx, biv::launch_sort(s.dp.ids, s.dp.wts, ne, k, T, s.dp, st), "dispatch");
+    MARK();
 
     biv::MvArgs a{};
     a.a = m->gate->m;
@@ -291,9 +366,11 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     a.u_max = std::min(ne, P);
     a.x_by_token = 1;
     HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
+    MARK();
 
     const int rows_act = has_shared ? P + T : P;
-    HIP_TRY(ctx, biv::launch_quant_rows(s.act, rows_act * ff / 32, s.aq, s.ad, s.as, st), "quantise act");
+    HIP_TRY(ctx, biv::launch_quant_rows(s.act, rows_act * ff / 32, ff, s.aq, s.ad, s.as, st), "quantise act");
+    MARK();
 
     biv::MvArgs d{};
     d.a = m->down->m;
@@ -309,10 +386,13 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     d.u_max = std::min(ne, P);
     d.x_by_token = 0;
     HIP_TRY(ctx, biv::launch_down(d, st), "expert down");
+    MARK();
 
     HIP_TRY(ctx,
             biv::launch_combine(s.y, s.dp, s.glogit, has_shared, T, P, k, E, out, (flags & BIV_HIP_ADD) != 0, st),
             "combine");
+    MARK();
+#undef MARK
     return 0;
 }
 
@@ -354,6 +434,9 @@ void biv_hip_destroy(biv_hip_ctx *ctx)
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     scratch_free(ctx);
+    for (auto &v : ctx->ev_fwd)
+        for (auto e : v) (void)hipEventDestroy(e);
+    for (auto e : ctx->ev_pool) (void)hipEventDestroy(e);
     for (void *p : ctx->allocs) (void)hipFree(p);
     for (auto *w : ctx->weights) delete w;
     for (auto *x : ctx->experts) delete x;
@@ -503,6 +586,7 @@ int biv_hip_moe_forward_taps(biv_hip_ctx *ctx, const biv_hip_moe *moe, const flo
         HIP_TRY(ctx, hipMemcpyAsync(s.o_stage, out, sizeof(float) * n * E, hipMemcpyHostToDevice, ctx->stream),
                 "copy x");
     Dumps dm;
+    bool permuted_acts = false;
     std::vector<void *> tmp;
     auto dev = [&](size_t bytes) -> int32_t * {
         void *p = nullptr;
@@ -532,11 +616,31 @@ int biv_hip_moe_forward_taps(biv_hip_ctx *ctx, const biv_hip_moe *moe, const flo
         d2h(taps->up_idots, dm.up, sizeof(int32_t) * R * ff * (E / 32));
         d2h(taps->act_q, s.aq, R * ff);
         d2h(taps->act_d, s.ad, sizeof(float) * R * ff / 32);
+        permuted_acts = taps->act_q || taps->act_d;
         d2h(taps->down_idots, dm.down, sizeof(int32_t) * R * E * (ff / 32));
     }
     hipError_t e = hipStreamSynchronize(ctx->stream);
     for (void *p : tmp) (void)hipFree(p);
     if (!rc && e != hipSuccess) rc = hip_fail(ctx, e, "forward");
+    if (!rc && permuted_acts) {
+        // the intermediate is stored in the chain layout: back to row order
+        const int K = (int)ff;
+        std::vector<int8_t> qrow(ff);
+        std::vector<float> drow(ff / 32);
+        for (size_t r = 0; r < R; r++) {
+            if (taps->act_q) {
+                int8_t *row = taps->act_q + r * ff;
+                memcpy(qrow.data(), row, ff);
+                for (int b = 0; b < K / 32; b++)
+                    for (int l = 0; l < 8; l++) memcpy(row + 32 * b + 4 * l, &qrow[4 * biv::lay::q8_word(b, l)], 4);
+            }
+            if (taps->act_d) {
+                float *row = taps->act_d + r * (ff / 32);
+                memcpy(drow.data(), row, sizeof(float) * (ff / 32));
+                for (int b = 0; b < K / 32; b++) row[b] = drow[biv::lay::q8_scale(K, b)];
+            }
+        }
+    }
     return rc;
 }
 
@@ -587,5 +691,30 @@ int biv_hip_numerics(const biv_hip_ctx *ctx, char *buf, size_t len)
 }
 
 size_t biv_hip_device_bytes(const biv_hip_ctx *ctx) { return ctx ? ctx->bytes : 0; }
+
+int biv_hip_set_timing(biv_hip_ctx *ctx, int enable)
+{
+    if (!ctx) return BIV_HIP_E_INVALID;
+    ctx->timing = enable != 0;
+    return 0;
+}
+
+int biv_hip_stage_times(biv_hip_ctx *ctx, double *ms, int n_stages, int *n_forwards)
+{
+    if (!ctx || !ms || n_stages < N_STAGES) return BIV_HIP_E_INVALID;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "sync");
+    for (int i = 0; i < n_stages; i++) ms[i] = 0.0;
+    for (auto &v : ctx->ev_fwd) {
+        for (int i = 0; i < N_STAGES; i++) {
+            float t = 0.0f;
+            HIP_TRY(ctx, hipEventElapsedTime(&t, v[i], v[i + 1]), "event time");
+            ms[i] += t;
+        }
+        for (auto e : v) ctx->ev_pool.push_back(e);
+    }
+    if (n_forwards) *n_forwards = (int)ctx->ev_fwd.size();
+    ctx->ev_fwd.clear();
+    return 0;
+}
 
 } // extern "C"

@@ -10,18 +10,18 @@ namespace biv {
 enum : int { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4K = 12, T_Q6K = 14, T_BF16 = 30 };
 
 // One matrix, or a stack of n matrices of rows x cols, in device memory,
-// repacked at upload into planes whose rows start on 16-byte boundaries so
-// that every kernel reads them with 128-bit loads.  The bytes per element are
-// those of the ggml type: repacking moves bytes, it adds none.
-//   Q8_0: q = int8  [n][rows][cols]              the 32 quants of each block
-//         s = f16   [n][rows][cols/32]           the block scales
-//   Q4_K: q = uint8 [n][rows][cols/2]            ggml's nibble packing, per super-block
+// repacked at upload into planes whose rows start on 16-byte boundaries and
+// whose words sit in the chain layouts of layout.hpp.  The bytes per element
+// are those of the ggml type: repacking moves bytes, it adds none.
+//   Q8_0: q = int8  [n][rows][cols]              the quants, lay::q8_word order
+//         s = f16   [n][rows][cols/32]           block scales, lay::q8_scale order
+//   Q4_K: q = uint8 [n][rows][cols/2]            the nibble bytes, lay::q4k_word order
 //         s = uint8 [n][rows][cols/256][16]      d, dmin (f16) and the 12 packed scale bytes
-//   Q6_K: q = uint8 [n][rows][cols/256][192]     ql (128 B) then qh (64 B), as in ggml
-//         s = int8  [n][rows][cols/256][16]      sub-block scales
-//         d = f16   [n][rows][cols/256]          super-block scale
+//   Q6_K: q = uint8 [n][rows][cols/256 * 192]    ql words (lay::q6k_ql_word), then qh (lay::q6k_qh_word)
+//         s = int8  [n][rows][cols/16]           sub-block scales, lay::q6k_sc order
+//         d = f16   [n][rows][cols/256]          super-block scales
 //   BF16: q = uint16[n][rows][cols]
-//   F32:  q = float [n][rows][cols]
+//   F32:  q = float [n][rows][cols]              lay::f32_elem order
 struct DevMat {
     int ty = -1;
     int cols = 0, rows = 0, n = 0;
@@ -45,7 +45,7 @@ struct Dispatch {
 };
 
 // Launchers (kernels.hip).  All enqueue on `st`; none synchronises.
-hipError_t launch_quant_rows(const float *x, int n_blocks, int8_t *qs, float *d, float *s, hipStream_t st);
+hipError_t launch_quant_rows(const float *x, int n_blocks, int K, int8_t *qs, float *d, float *s, hipStream_t st);
 hipError_t launch_router(const float *router, const float *gate_inp, int n_expert, int E, const float *h, int T,
                          float *logits, float *glogit, hipStream_t st);
 hipError_t launch_route(const float *logits, int n_expert, int k, int T, int *ids, float *wts, hipStream_t st);

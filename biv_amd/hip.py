@@ -29,7 +29,10 @@ SYMBOLS = [
     "biv_hip_upload_weight", "biv_hip_upload_experts", "biv_hip_moe_create", "biv_hip_moe_forward",
     "biv_hip_moe_forward_device", "biv_hip_moe_forward_taps", "biv_hip_malloc", "biv_hip_free",
     "biv_hip_memcpy_h2d", "biv_hip_memcpy_d2h", "biv_hip_numerics", "biv_hip_device_bytes",
+    "biv_hip_set_timing", "biv_hip_stage_times",
 ]
+
+STAGES = ["quant_h", "router", "route", "dispatch", "gate_up", "quant_act", "down", "combine"]
 
 
 class HipError(RuntimeError):
@@ -77,6 +80,8 @@ def load():
     L.biv_hip_numerics.argtypes = [vp, ctypes.c_char_p, sz]
     L.biv_hip_device_bytes.argtypes = [vp]
     L.biv_hip_device_bytes.restype = sz
+    L.biv_hip_set_timing.argtypes = [vp, i]
+    L.biv_hip_stage_times.argtypes = [vp, ctypes.POINTER(ctypes.c_double), i, ctypes.POINTER(ctypes.c_int)]
     _lib = L
     return L
 
@@ -222,3 +227,13 @@ class HipEngine:
 
     def device_bytes(self):
         return self.L.biv_hip_device_bytes(self.h)
+
+    def set_timing(self, enable):
+        self._check(self.L.biv_hip_set_timing(self.h, 1 if enable else 0))
+
+    def stage_times(self):
+        """(summed ms per stage, number of forwards) since the last call."""
+        ms = (ctypes.c_double * len(STAGES))()
+        n = ctypes.c_int()
+        self._check(self.L.biv_hip_stage_times(self.h, ms, len(STAGES), ctypes.byref(n)))
+        return dict(zip(STAGES, list(ms))), n.value

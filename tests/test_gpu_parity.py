@@ -5,7 +5,8 @@ The bar, per forward on the same seeded inputs:
   - top-k expert ids identical, weights within 1e-5 relative
   - every per-32-block int32 dot of gate, up and down bit-identical to the
     oracle's integer dot of the same weight row and int8 activations
-  - block output within max|d| <= 1e-3 * RMS(output)
+  - block output within max|d| <= 1e-3 * RMS(output), and in fact
+    bit-identical to the oracle's (>= 99.99% of outputs asserted, 100% seen)
   - bit-identical from run to run, and a token's output independent of the
     other tokens in its batch
 """
@@ -39,10 +40,17 @@ def layer_for(engine, **kw):
     return _layers[key]
 
 
-def check_output(ref, got, tol=TOL):
+def check_output(ref, got, tol=TOL, min_exact=0.9999):
+    """max|d| <= tol * RMS (the north star's bar); and, since every sum runs
+    in the reference's order and exp is glibc's to the bit, the outputs carry
+    the reference's exact bits (measured: all of them; the bar leaves room for
+    the 2 in 2.2e9 inputs where the restated expf is one ulp off)."""
     rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
     err = float(np.abs(ref.astype(np.float64) - got).max())
+    exact = float(np.mean(ref.view(np.uint32) == got.view(np.uint32)))
+    print(f"max|d|/RMS = {err / rms:.2e}, bit-identical fraction = {exact:.6f}")
     assert err <= tol * rms, f"max|d| {err:.3e} > {tol} * RMS {rms:.3e}"
+    assert exact >= min_exact, f"only {exact:.4f} of outputs bit-identical"
     return err / rms
 
 
@@ -177,7 +185,7 @@ def test_no_shared_expert_and_add(orc, engine):
     x = synth.make_tokens(10, 3)
     ref = orc.moe(layer, h)
     got = moe.ffn(h, out=x.copy(), add=True)
-    check_output(ref, got - x, tol=2 * TOL)
+    check_output(ref, got - x, tol=2 * TOL, min_exact=0.0)
     assert np.array_equal(got.view(np.uint32), (x + moe.ffn(h)).view(np.uint32))
 
 
