@@ -45,18 +45,18 @@ def stage_bytes(stage, U, T):
     read and written once)."""
     P = T * K
     R = P + T
-    if stage == "gate_up":
+    if stage == "gate_up":  # weights, Q8 h, the f32 intermediate
         return (U + 1) * 2 * FF * Q8_ROW_E + T * E * 9 // 8 + R * FF * 4
-    if stage == "down":
-        return (U + 1) * E * Q8_ROW_FF + R * FF * 9 // 8 + R * E * 4
-    if stage == "router":
-        return ROUTER_BYTES + T * E * 4 + T * (NE + 1) * 4
-    if stage == "combine":
-        return R * E * 4 + T * E * 4 + P * 8
-    if stage == "quant_h":
-        return T * E * 4 + T * E * 9 // 8
     if stage == "quant_act":
         return R * FF * 4 + R * FF * 9 // 8
+    if stage == "down":  # weights, Q8 intermediate, y
+        return (U + 1) * E * Q8_ROW_FF + R * FF * 9 // 8 + R * E * 4
+    if stage == "combine":
+        return R * E * 4 + T * E * 4 + P * 8
+    if stage == "router":  # router + gate_inp, h, logits, Q8 h
+        return ROUTER_BYTES + T * E * 4 + T * (NE + 1) * 4 + T * E * 9 // 8
+    if stage == "route_sort":
+        return T * NE * 4 + P * 24
     return 0
 
 

@@ -42,6 +42,7 @@ struct Scratch {
     float *ad = nullptr, *as = nullptr;
     float *y = nullptr;
     float *h_stage = nullptr, *o_stage = nullptr;
+    int *counters = nullptr;
     biv::Dispatch dp{};
 };
 
@@ -267,16 +268,22 @@ int scratch_fit(biv_hip_ctx *ctx, const biv_hip_moe *m, int T)
     rc = rc ? rc : sc_alloc(ctx, R * E, &s.y);
     rc = rc ? rc : sc_alloc(ctx, cap * E, &s.h_stage);
     rc = rc ? rc : sc_alloc(ctx, cap * E, &s.o_stage);
-    rc = rc ? rc : sc_alloc(ctx, 1, &s.dp.n_active);
-    rc = rc ? rc : sc_alloc(ctx, ne, &s.dp.act_expert);
-    rc = rc ? rc : sc_alloc(ctx, ne, &s.dp.act_beg);
-    rc = rc ? rc : sc_alloc(ctx, ne, &s.dp.act_cnt);
+    rc = rc ? rc : sc_alloc(ctx, 1, &s.dp.n_slots);
+    rc = rc ? rc : sc_alloc(ctx, ne + P, &s.dp.sl_expert);
+    rc = rc ? rc : sc_alloc(ctx, ne + P, &s.dp.sl_beg);
+    rc = rc ? rc : sc_alloc(ctx, ne + P, &s.dp.sl_cnt);
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_tok);
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_exp);
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_w);
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.tok_pairs);
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.ids);
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.wts);
+    rc = rc ? rc : sc_alloc(ctx, biv::n_counters(), &s.counters);
+    if (!rc) {
+        // the finishing-workgroup tickets start at zero; kernels reset them after use
+        hipError_t e = hipMemset(s.counters, 0, sizeof(int) * biv::n_counters());
+        if (e != hipSuccess) rc = hip_fail(ctx, e, "clear counters");
+    }
     if (rc) {
         scratch_free(ctx);
         return rc;
@@ -289,7 +296,7 @@ struct Dumps {
     int32_t *gate = nullptr, *up = nullptr, *down = nullptr;
 };
 
-constexpr int N_STAGES = 8; // quantise h, router, route, dispatch, gate/up, quantise act, down, combine
+constexpr int N_STAGES = 6; // router (+ quantise h), route + dispatch, gate/up, quantise act, down, combine
 
 // The stage markers of one forward when timing is on.
 struct StageMarks {
@@ -333,18 +340,28 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     const int E = m->E, ff = m->ff, ne = m->n_expert, k = m->k;
     const int P = T * k;
     const bool has_shared = m->sg != nullptr;
+    int *ctr_rs = s.counters;
+    // pairs per slot: decode keeps an expert's tokens together; larger passes
+    // cut them so that hot experts and the shared expert spread over the GPU
+    const int chunk = T <= 64 ? 64 : 16;
+    const int u_max = biv::max_slots(ne, P, chunk);
+
+    biv::RouterArgs ra{};
+    ra.router = reinterpret_cast<const float *>(m->router->m.q);
+    ra.gate_inp = has_shared ? reinterpret_cast<const float *>(m->gi->m.q) : nullptr;
+    ra.n_expert = ne;
+    ra.E = E;
+    ra.T = T;
+    ra.h = h;
+    ra.logits = s.logits;
+    ra.glogit = s.glogit;
+    ra.xq = s.xq;
+    ra.xd = s.xd;
+    ra.xs = s.xs;
     MARK();
-    HIP_TRY(ctx, biv::launch_quant_rows(h, T * E / 32, E, s.xq, s.xd, s.xs, st), "quantise h");
+    HIP_TRY(ctx, biv::launch_router(ra, st), "router");
     MARK();
-    HIP_TRY(ctx,
-            biv::launch_router(reinterpret_cast<const float *>(m->router->m.q),
-                               has_shared ? reinterpret_cast<const float *>(m->gi->m.q) : nullptr, ne, E, h, T,
-                               s.logits, s.glogit, st),
-            "router");
-    MARK();
-    HIP_TRY(ctx, biv::launch_route(s.logits, ne, k, T, s.dp.ids, s.dp.wts, st), "route");
-    MARK();
-    HIP_TRY(ctx, biv::launch_sort(s.dp.ids, s.dp.wts, ne, k, T, s.dp, st), "dispatch");
+    HIP_TRY(ctx, biv::launch_route_sort(s.logits, ne, k, T, chunk, s.dp, ctr_rs, st), "route and dispatch");
     MARK();
 
     biv::MvArgs a{};
@@ -363,11 +380,11 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     a.dump_b = dm.up;
     a.T = T;
     a.P = P;
-    a.u_max = std::min(ne, P);
+    a.u_max = u_max;
+    a.chunk = chunk;
     a.x_by_token = 1;
     HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
     MARK();
-
     const int rows_act = has_shared ? P + T : P;
     HIP_TRY(ctx, biv::launch_quant_rows(s.act, rows_act * ff / 32, ff, s.aq, s.ad, s.as, st), "quantise act");
     MARK();
@@ -383,11 +400,11 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     d.dump_a = dm.down;
     d.T = T;
     d.P = P;
-    d.u_max = std::min(ne, P);
+    d.u_max = u_max;
+    d.chunk = chunk;
     d.x_by_token = 0;
     HIP_TRY(ctx, biv::launch_down(d, st), "expert down");
     MARK();
-
     HIP_TRY(ctx,
             biv::launch_combine(s.y, s.dp, s.glogit, has_shared, T, P, k, E, out, (flags & BIV_HIP_ADD) != 0, st),
             "combine");

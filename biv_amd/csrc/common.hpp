@@ -31,11 +31,14 @@ struct DevMat {
 };
 
 // Routing and dispatch state of one forward of T tokens (device pointers).
+// A slot is a run of at most `chunk` consecutive pairs of one expert; an
+// expert with more pairs has several slots.  Slots are in ascending expert
+// order.
 struct Dispatch {
-    int *n_active;   // [1]  U: experts with at least one pair
-    int *act_expert; // [n_expert] expert of active slot u, ascending
-    int *act_beg;    // [n_expert] first dispatch position of slot u
-    int *act_cnt;    // [n_expert] pairs of slot u
+    int *n_slots;    // [1] slots of the routed experts
+    int *sl_expert;  // [max slots] expert of slot u
+    int *sl_beg;     // [max slots] first dispatch position of slot u
+    int *sl_cnt;     // [max slots] pairs of slot u (<= chunk)
     int *pair_tok;   // [P] token of each pair in dispatch order
     int *pair_exp;   // [P] expert of each pair in dispatch order
     float *pair_w;   // [P] routing weight of each pair
@@ -45,24 +48,46 @@ struct Dispatch {
 };
 
 // Launchers (kernels.hip).  All enqueue on `st`; none synchronises.
-hipError_t launch_quant_rows(const float *x, int n_blocks, int K, int8_t *qs, float *d, float *s, hipStream_t st);
-hipError_t launch_router(const float *router, const float *gate_inp, int n_expert, int E, const float *h, int T,
-                         float *logits, float *glogit, hipStream_t st);
-hipError_t launch_route(const float *logits, int n_expert, int k, int T, int *ids, float *wts, hipStream_t st);
-hipError_t launch_sort(const int *ids, const float *wts, int n_expert, int k, int T, const Dispatch &dp,
-                       hipStream_t st);
+//
+// A forward is six launches: router (with the quantisation of h); route and
+// dispatch sort; gate/up; quantisation of the intermediate; down; combine.
+// The dispatch sort needs every token routed: the workgroup that finishes
+// routing last does it, found with an integer ticket counter (the result does
+// not depend on which workgroup that is).  The counter starts at zero
+// (cleared when the scratch is allocated) and that workgroup puts it back.
+
+struct RouterArgs {
+    const float *router;   // [n_expert][E], f32 chain layout
+    const float *gate_inp; // [E] or nullptr
+    int n_expert, E, T;
+    const float *h;        // [T][E]
+    float *logits;         // [T][n_expert]
+    float *glogit;         // [T]
+    int8_t *xq;            // h quantised: [T][E] chain layout
+    float *xd, *xs;        // [T][E/32]
+};
+// router logits + gate_inp logit + Q8 quantisation of h
+hipError_t launch_router(const RouterArgs &a, hipStream_t st);
+// route every token, then sort the pairs into dispatch order
+hipError_t launch_route_sort(const float *logits, int n_expert, int k, int T, int chunk, const Dispatch &dp,
+                             int *counter, hipStream_t st);
+
+// upper bound of the routed slots of T tokens: one partial slot per expert plus P / chunk full ones
+inline int max_slots(int n_expert, int P, int chunk) { return (n_expert < P ? n_expert : P) + P / chunk; }
 
 struct MvArgs {
     DevMat a, b;            // routed stacks (b: the up stack of a gate/up pair)
     DevMat sa, sb;          // the shared expert's matrices (n = 1), sa.q == nullptr without one
-    const int8_t *xq;       // input rows: int8 [rows_in][K]
+    const int8_t *xq;       // input rows: int8 [rows_in][K], chain layout
     const float *xd;        // [rows_in][K/32] block scales
     const float *xs;        // [rows_in][K/32] block d * sum(q) (Q4_K mins)
     Dispatch dp;
     float *out;             // [P + T][rows]
     int32_t *dump_a;        // optional [P + T][rows][K/32] block int32 dots of a
     int32_t *dump_b;        // optional, of b
-    int T, P, u_max;
+    int T, P;
+    int u_max;              // grid slots of the routed experts (max_slots); the shared expert's follow
+    int chunk;              // pairs per slot; the shared expert's T tokens are cut the same way
     int x_by_token;         // 1: input row of a pair is its token's (gate/up); 0: the pair's own (down)
 };
 
@@ -70,10 +95,13 @@ struct MvArgs {
 hipError_t launch_gateup(const MvArgs &a, hipStream_t st);
 // down: out[p][r] = down_r . x_p
 hipError_t launch_down(const MvArgs &a, hipStream_t st);
-
+// Q8Act of n_blocks 32-element blocks of rows of K, into the chain layout
+hipError_t launch_quant_rows(const float *x, int n_blocks, int K, int8_t *qs, float *d, float *s, hipStream_t st);
 // out[t] (+)= sum over t's pairs, ascending expert, of w * y[pair], then
 // sigmoid(glogit[t]) * y[P + t] when there is a shared expert.
-hipError_t launch_combine(const float *y, const Dispatch &dp, const float *glogit, int has_shared, int T, int P,
-                          int k, int E, float *out, int add, hipStream_t st);
+hipError_t launch_combine(const float *y, const Dispatch &dp, const float *glogit, int has_shared, int T, int P, int k,
+                          int E, float *out, int add, hipStream_t st);
+
+inline size_t n_counters() { return 1; }
 
 } // namespace biv

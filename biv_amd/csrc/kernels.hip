@@ -61,35 +61,19 @@ template <int N> __device__ inline void ld_words(const void *p, int (&out)[N])
 }
 
 // ---------------------------------------------------------------------------
-// Q8Act::quantize_into (quant.rs:368-394), one thread per 32-element block of
-// row-major x [rows][K]: amax, d = amax / 127, id = 1/d (0 when d is 0),
-// q = round-half-away(v * id), s = d * sum(q); IEEE division and no
-// contraction keep it bit-exact.  Written in the chain layout (layout.hpp).
-__global__ __launch_bounds__(256) void k_quant_rows(const float *__restrict__ x, int n_blocks, int K,
-                                                    int8_t *__restrict__ qs, float *__restrict__ d,
-                                                    float *__restrict__ s)
+// Q8Act::quantize_into (quant.rs:368-394) of one 32-element block v of row
+// `row`: amax, d = amax / 127, id = 1/d (0 when d is 0), q =
+// round-half-away(v * id), s = d * sum(q); IEEE division and no contraction
+// keep it bit-exact.  Written in the chain layout (layout.hpp).
+__device__ inline void quant_block(const float (&v)[32], int K, size_t row, int b, int8_t *qs, float *d, float *s)
 {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n_blocks) return;
-    const int nb = K / 32;
-    const int row = i / nb, b = i % nb;
-    const float4 *xb = reinterpret_cast<const float4 *>(x + 32 * (size_t)i);
-    float v[32];
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        float4 f = xb[j];
-        v[4 * j] = f.x;
-        v[4 * j + 1] = f.y;
-        v[4 * j + 2] = f.z;
-        v[4 * j + 3] = f.w;
-    }
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
     const float db = amax / 127.0f;
     const float id = db != 0.0f ? 1.0f / db : 0.0f;
     int sum = 0;
-    int *qrow = reinterpret_cast<int *>(qs + (size_t)row * K);
+    int *qrow = reinterpret_cast<int *>(qs + row * K);
 #pragma unroll
     for (int l = 0; l < 8; l++) {
         unsigned w = 0;
@@ -101,8 +85,40 @@ __global__ __launch_bounds__(256) void k_quant_rows(const float *__restrict__ x,
         }
         qrow[lay::q8_word(b, l)] = (int)w;
     }
-    d[(size_t)row * nb + lay::q8_scale(K, b)] = db;
-    s[(size_t)row * nb + lay::q8_scale(K, b)] = db * (float)sum;
+    d[row * (K / 32) + lay::q8_scale(K, b)] = db;
+    s[row * (K / 32) + lay::q8_scale(K, b)] = db * (float)sum;
+}
+
+// 32 consecutive floats, 16-byte aligned
+__device__ inline void load32(const float *p, float (&v)[32])
+{
+    const float4 *q = reinterpret_cast<const float4 *>(p);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        float4 f = q[j];
+        v[4 * j] = f.x;
+        v[4 * j + 1] = f.y;
+        v[4 * j + 2] = f.z;
+        v[4 * j + 3] = f.w;
+    }
+}
+
+// The caller's workgroup takes a ticket on *counter after its threads are
+// done; true in the workgroup whose ticket is total - 1, which then sees every
+// other workgroup's writes and puts the counter back to zero.
+__device__ inline bool finishing_workgroup(int *counter, int total)
+{
+    __shared__ int last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        const int ticket = atomicAdd(counter, 1);
+        last = ticket == total - 1;
+        if (last) atomicExch(counter, 0);
+    }
+    __syncthreads();
+    if (last) __threadfence();
+    return last;
 }
 
 // ---------------------------------------------------------------------------
@@ -111,12 +127,23 @@ __global__ __launch_bounds__(256) void k_quant_rows(const float *__restrict__ x,
 // wave runs FMA chain L over elements L, L+32, ... of one row; then the tree
 // (acc0+acc1)+(acc2+acc3) and hsum (quant.rs:1149-1153).  Rows are stored in
 // the f32 chain layout, so each lane's 4-value steps are one 128-bit load.
-template <int NS, int TC>
-__global__ __launch_bounds__(256) void k_router(const float *__restrict__ router, const float *__restrict__ gate_inp,
-                                                int n_expert, const float *__restrict__ h, int T,
-                                                float *__restrict__ logits, float *__restrict__ glogit)
+template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(RouterArgs a)
 {
     constexpr int E = 32 * NS;
+    const float *__restrict__ router = a.router;
+    const float *__restrict__ gate_inp = a.gate_inp;
+    const float *__restrict__ h = a.h;
+    const int n_expert = a.n_expert, T = a.T;
+    // the Q8 activations of h, for the experts: every thread of the grid
+    // takes blocks of 32 in turn
+    {
+        const int nthreads = gridDim.x * gridDim.y * blockDim.x;
+        for (int i = (blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < T * (E / 32); i += nthreads) {
+            float v[32];
+            load32(h + 32 * (size_t)i, v);
+            quant_block(v, E, i / (E / 32), i % (E / 32), a.xq, a.xd, a.xs);
+        }
+    }
     const int L = threadIdx.x & 31;
     const int row = blockIdx.x * (blockDim.x / 32) + (threadIdx.x >> 5);
     const bool valid = row < n_expert || (row == n_expert && gate_inp != nullptr);
@@ -149,8 +176,8 @@ __global__ __launch_bounds__(256) void k_router(const float *__restrict__ router
         v = v + __shfl_xor(v, 2);  // movehl
         v = v + __shfl_xor(v, 1);  // movehdup
         if (valid && L == 0) {
-            if (row < n_expert) logits[(size_t)t * n_expert + row] = v;
-            else glogit[t] = v;
+            if (row < n_expert) a.logits[(size_t)t * n_expert + row] = v;
+            else a.glogit[t] = v;
         }
     }
 }
@@ -162,12 +189,10 @@ __global__ __launch_bounds__(256) void k_router(const float *__restrict__ router
 // token, up to 8 logits per lane.
 __device__ inline bool better(float pa, int ia, float pb, int ib) { return pa > pb || (pa == pb && ia < ib); }
 
-__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits, int n_expert, int k, int T,
-                                               int *__restrict__ ids, float *__restrict__ wts)
+__device__ void route_token(const float *__restrict__ logits, int n_expert, int k, int t, int *__restrict__ ids,
+                            float *__restrict__ wts)
 {
     const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x >> 6);
-    if (t >= T) return;
     constexpr int PER = 8;
     float v[PER];
     float mx = -INFINITY;
@@ -252,51 +277,64 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
 // kernels.metal:1675-1739).  Counts are integer atomics in LDS, whose result
 // does not depend on their order; a pair's place among its expert's pairs is
 // the number of earlier tokens with that expert, read from a token bitmap, so
-// the order is deterministic.  One workgroup of 1024 threads.
-constexpr int SORT_THREADS = 1024;
+// the order is deterministic.  Run by one workgroup of NT threads.
 constexpr int MAX_EXPERTS = 256;
+constexpr int RS_THREADS = 256;
 
-__global__ __launch_bounds__(SORT_THREADS) void k_sort(const int *__restrict__ ids, const float *__restrict__ wts,
-                                                       int n_expert, int k, int T, Dispatch dp)
+// Inclusive scan of v over the MAX_EXPERTS first threads (all threads call it).
+template <int NT> __device__ inline int scan_experts(int v, int *buf)
 {
+    const int tid = threadIdx.x;
+    if (tid < MAX_EXPERTS) buf[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < MAX_EXPERTS; off <<= 1) {
+        int add = (tid < MAX_EXPERTS && tid >= off) ? buf[tid - off] : 0;
+        __syncthreads();
+        if (tid < MAX_EXPERTS) buf[tid] += add;
+        __syncthreads();
+    }
+    const int r = tid < MAX_EXPERTS ? buf[tid] : 0;
+    __syncthreads();
+    return r;
+}
+
+template <int NT>
+__device__ void sort_pairs(const int *__restrict__ ids, const float *__restrict__ wts, int n_expert, int k, int T,
+                           int chunk, const Dispatch &dp)
+{
+    static_assert(NT >= MAX_EXPERTS, "one thread per expert");
     __shared__ int cnt[MAX_EXPERTS];
     __shared__ int scan[MAX_EXPERTS];
     __shared__ int run[MAX_EXPERTS];
-    __shared__ unsigned bm[MAX_EXPERTS][SORT_THREADS / 32];
+    __shared__ unsigned bm[MAX_EXPERTS][NT / 32];
     const int tid = threadIdx.x;
     const int P = T * k;
-    for (int e = tid; e < MAX_EXPERTS; e += SORT_THREADS) {
+    for (int e = tid; e < MAX_EXPERTS; e += NT) {
         cnt[e] = 0;
         run[e] = 0;
     }
-    for (int i = tid; i < MAX_EXPERTS * (SORT_THREADS / 32); i += SORT_THREADS) (&bm[0][0])[i] = 0u;
+    for (int i = tid; i < MAX_EXPERTS * (NT / 32); i += NT) (&bm[0][0])[i] = 0u;
     __syncthreads();
-    for (int i = tid; i < P; i += SORT_THREADS) atomicAdd(&cnt[ids[i]], 1); // ids < n_expert (k_route)
+    for (int i = tid; i < P; i += NT) atomicAdd(&cnt[ids[i]], 1); // ids < n_expert (route_token)
     __syncthreads();
-    // inclusive scan of (active << 20 | count): expert offsets and active slots at once
-    if (tid < MAX_EXPERTS) scan[tid] = tid < n_expert ? ((cnt[tid] > 0) << 20) | cnt[tid] : 0;
-    __syncthreads();
-    for (int off = 1; off < MAX_EXPERTS; off <<= 1) {
-        int add = (tid < MAX_EXPERTS && tid >= off) ? scan[tid - off] : 0;
-        __syncthreads();
-        if (tid < MAX_EXPERTS) scan[tid] += add;
-        __syncthreads();
-    }
+    // offsets of the experts' pairs, and of their slots
+    const int c = tid < n_expert ? cnt[tid] : 0;
+    const int nsl = (c + chunk - 1) / chunk;
+    const int pos_incl = scan_experts<NT>(c, scan);
+    const int sl_incl = scan_experts<NT>(nsl, scan);
     if (tid < n_expert) {
-        int c = cnt[tid];
-        int incl = scan[tid];
-        int beg = (incl & 0xFFFFF) - c;
-        if (c > 0) {
-            int u = (incl >> 20) - 1;
-            dp.act_expert[u] = tid;
-            dp.act_beg[u] = beg;
-            dp.act_cnt[u] = c;
+        const int beg = pos_incl - c;
+        for (int j = 0; j < nsl; j++) {
+            const int u = sl_incl - nsl + j;
+            dp.sl_expert[u] = tid;
+            dp.sl_beg[u] = beg + j * chunk;
+            dp.sl_cnt[u] = min(chunk, c - j * chunk);
         }
         cnt[tid] = beg; // from here on: the expert's first position
     }
-    if (tid == 0) *dp.n_active = scan[MAX_EXPERTS - 1] >> 20;
+    if (tid == MAX_EXPERTS - 1) *dp.n_slots = sl_incl;
     __syncthreads();
-    for (int c0 = 0; c0 < T; c0 += SORT_THREADS) {
+    for (int c0 = 0; c0 < T; c0 += NT) {
         const int t = c0 + tid;
         const int word = tid >> 5;
         const unsigned bit = 1u << (tid & 31);
@@ -329,7 +367,7 @@ __global__ __launch_bounds__(SORT_THREADS) void k_sort(const int *__restrict__ i
         __syncthreads();
         if (tid < MAX_EXPERTS) {
             int add = 0;
-            for (int w = 0; w < SORT_THREADS / 32; w++) {
+            for (int w = 0; w < NT / 32; w++) {
                 add += __popc(bm[tid][w]);
                 bm[tid][w] = 0u;
             }
@@ -337,6 +375,16 @@ __global__ __launch_bounds__(SORT_THREADS) void k_sort(const int *__restrict__ i
         }
         __syncthreads();
     }
+}
+
+// One wavefront per token routes it; the workgroup that finishes last sorts.
+__global__ __launch_bounds__(RS_THREADS) void k_route_sort(const float *__restrict__ logits, int n_expert, int k,
+                                                           int T, int chunk, Dispatch dp, int *counter)
+{
+    const int t = blockIdx.x * (RS_THREADS / WAVE) + (threadIdx.x >> 6);
+    if (t < T) route_token(logits, n_expert, k, t, dp.ids, dp.wts);
+    if (!finishing_workgroup(counter, gridDim.x)) return;
+    sort_pairs<RS_THREADS>(dp.ids, dp.wts, n_expert, k, T, chunk, dp);
 }
 
 // ---------------------------------------------------------------------------
@@ -518,6 +566,19 @@ __device__ inline float q4k_mins(const DevMat &M, size_t mrow, const float *xs, 
 }
 
 // ---------------------------------------------------------------------------
+// Combine for every token (model.rs:884-896): o = 0; for each of t's experts
+// in ascending id, o = fma(w, y, o) (quant::axpy, quant.rs:1209-1226); then
+// o = fma(sigmoid(g), y_shared, o); then out = o, or out += o (the residual
+// add of model.rs:790).
+struct CombineArgs {
+    const float *y;
+    Dispatch dp;
+    const float *glogit;
+    float *out;
+    int T, P, k, E, has_shared, add;
+};
+
+// ---------------------------------------------------------------------------
 // Grouped expert matvec.  blockIdx.y is an active-expert slot (or, at u_max,
 // the shared expert).  A wave is four 16-lane groups; a group runs the 16
 // chains of one (matrix, row): for gate/up, groups (row, gate) and (row, up)
@@ -534,16 +595,17 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane >> 4, ln = lane & 15, pi = ln >> 3, l = ln & 7;
     const int u = blockIdx.y;
-    const bool shared = u == a.u_max;
-    int e = 0, beg, cnt;
+    const bool shared = u >= a.u_max;
+    int e = 0, beg, cnt, tok0 = 0;
     if (shared) {
-        beg = a.P;
-        cnt = a.T;
+        tok0 = (u - a.u_max) * a.chunk; // the shared expert's tokens [tok0, tok0 + cnt)
+        beg = a.P + tok0;
+        cnt = min(a.chunk, a.T - tok0);
     } else {
-        if (u >= *a.dp.n_active) return; // uniform over the workgroup
-        e = a.dp.act_expert[u];
-        beg = a.dp.act_beg[u];
-        cnt = a.dp.act_cnt[u];
+        if (u >= *a.dp.n_slots) return; // uniform over the workgroup
+        e = a.dp.sl_expert[u];
+        beg = a.dp.sl_beg[u];
+        cnt = a.dp.sl_cnt[u];
     }
     const int m = GATEUP ? (grp & 1) : 0;
     const DevMat &M = GATEUP && m ? (shared ? a.sb : a.b) : (shared ? a.sa : a.a);
@@ -555,7 +617,7 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
     wc.load(M, mrow, pi, l);
     int32_t *dump = DUMP ? (m ? a.dump_b : a.dump_a) : nullptr;
     for (int i = 0; i < cnt; i++) {
-        const size_t xrow = a.x_by_token ? (size_t)(shared ? i : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
+        const size_t xrow = a.x_by_token ? (size_t)(shared ? tok0 + i : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
         const size_t orow = (size_t)(beg + i);
         XChain<K> xc;
         xc.load(a.xq, a.xd, xrow, pi, l);
@@ -591,28 +653,32 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
     }
 }
 
-// ---------------------------------------------------------------------------
-// Combine (model.rs:884-896): out[t] = 0; for each of t's experts in
-// ascending id, out = fma(w, y, out) (quant::axpy, quant.rs:1209-1226); then
-// out = fma(sigmoid(g), y_shared, out).  Then out is written or added.
-__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, Dispatch dp,
-                                                 const float *__restrict__ glogit, int has_shared, int T, int P,
-                                                 int k, int E, float *__restrict__ out, int add)
+// Q8Act of whole rows [rows][K] (the SwiGLU intermediate), one thread per block.
+__global__ __launch_bounds__(256) void k_quant_rows(const float *__restrict__ x, int n_blocks, int K,
+                                                    int8_t *__restrict__ qs, float *__restrict__ d,
+                                                    float *__restrict__ s)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_blocks) return;
+    float v[32];
+    load32(x + 32 * (size_t)i, v);
+    quant_block(v, K, i / (K / 32), i % (K / 32), qs, d, s);
+}
+
+// The combine as its own launch: grid (E / 256, T).
+__global__ __launch_bounds__(256) void k_combine(CombineArgs a)
 {
     const int t = blockIdx.y;
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= E) return;
+    if (c >= a.E) return;
     float o = 0.0f;
-    for (int j = 0; j < k; j++) {
-        int p = dp.tok_pairs[(size_t)t * k + j];
-        o = fmaf(dp.pair_w[p], y[(size_t)p * E + c], o);
+    for (int j = 0; j < a.k; j++) {
+        const int p = a.dp.tok_pairs[(size_t)t * a.k + j];
+        o = fmaf(a.dp.pair_w[p], a.y[(size_t)p * a.E + c], o);
     }
-    if (has_shared) {
-        const float sg = sigmoid(glogit[t]);
-        o = fmaf(sg, y[(size_t)(P + t) * E + c], o);
-    }
-    float *po = out + (size_t)t * E + c;
-    *po = add ? *po + o : o;
+    if (a.has_shared) o = fmaf(sigmoid(a.glogit[t]), a.y[(size_t)(a.P + t) * a.E + c], o);
+    float *po = a.out + (size_t)t * a.E + c;
+    *po = a.add ? *po + o : o;
 }
 
 // One launch over the routed slots (routed = 1) and/or the shared expert.
@@ -620,8 +686,8 @@ template <bool GATEUP, bool DUMP>
 hipError_t launch_mv_t(MvArgs a, int routed, int shared, hipStream_t st)
 {
     const DevMat &M = routed ? a.a : a.sa;
-    if (!routed) a.u_max = 0; // the only slot is the shared expert's
-    const int slots = (routed ? a.u_max : 0) + (shared ? 1 : 0);
+    if (!routed) a.u_max = 0; // the slots are the shared expert's
+    const int slots = (routed ? a.u_max : 0) + (shared ? (a.T + a.chunk - 1) / a.chunk : 0);
     if (slots == 0) return hipSuccess;
     const int rows_per_wg = MV_WAVES * (GATEUP ? 2 : 4);
     dim3 grid((M.rows + rows_per_wg - 1) / rows_per_wg, slots);
@@ -661,28 +727,16 @@ hipError_t launch_mv(const MvArgs &a, hipStream_t st)
 
 } // namespace
 
-hipError_t launch_quant_rows(const float *x, int n_blocks, int K, int8_t *qs, float *d, float *s, hipStream_t st)
+hipError_t launch_router(const RouterArgs &a, hipStream_t st)
 {
-    if (n_blocks <= 0) return hipSuccess;
-    k_quant_rows<<<(n_blocks + 255) / 256, 256, 0, st>>>(x, n_blocks, K, qs, d, s);
-    return hipGetLastError();
-}
-
-hipError_t launch_router(const float *router, const float *gate_inp, int n_expert, int E, const float *h, int T,
-                         float *logits, float *glogit, hipStream_t st)
-{
-    const int rows = n_expert + 1;
-    // small T: 2 rows per workgroup for many workgroups; large T: 8 rows per
-    // workgroup and tokens split over grid.y
-    const bool small = T <= 16;
-    const int rpw = small ? 2 : 8;
-    const int tc = small ? 16 : 32;
-    dim3 grid((rows + rpw - 1) / rpw, (T + tc - 1) / tc);
-    dim3 block(32 * rpw);
+    const int rows = a.n_expert + 1;
+    // 8 rows per workgroup; tokens split over grid.y in chunks of TC
+    const int tc = a.T <= 16 ? 16 : 32;
+    dim3 grid((rows + 7) / 8, (a.T + tc - 1) / tc);
 #define BIV_ROUTER_CASE(NS)                                                                                     \
-    if (E == 32 * NS) {                                                                                         \
-        if (small) k_router<NS, 16><<<grid, block, 0, st>>>(router, gate_inp, n_expert, h, T, logits, glogit);  \
-        else k_router<NS, 32><<<grid, block, 0, st>>>(router, gate_inp, n_expert, h, T, logits, glogit);        \
+    if (a.E == 32 * NS) {                                                                                       \
+        if (tc == 16) k_router<NS, 16><<<grid, 256, 0, st>>>(a);                                                \
+        else k_router<NS, 32><<<grid, 256, 0, st>>>(a);                                                         \
         return hipGetLastError();                                                                               \
     }
     BIV_ROUTER_CASE(64)
@@ -692,29 +746,32 @@ hipError_t launch_router(const float *router, const float *gate_inp, int n_exper
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_route(const float *logits, int n_expert, int k, int T, int *ids, float *wts, hipStream_t st)
+hipError_t launch_route_sort(const float *logits, int n_expert, int k, int T, int chunk, const Dispatch &dp,
+                             int *counter, hipStream_t st)
 {
-    k_route<<<(T + 3) / 4, 256, 0, st>>>(logits, n_expert, k, T, ids, wts);
+    k_route_sort<<<(T + RS_THREADS / WAVE - 1) / (RS_THREADS / WAVE), RS_THREADS, 0, st>>>(logits, n_expert, k, T,
+                                                                                           chunk, dp, counter);
     return hipGetLastError();
 }
 
-hipError_t launch_sort(const int *ids, const float *wts, int n_expert, int k, int T, const Dispatch &dp,
-                       hipStream_t st)
+hipError_t launch_quant_rows(const float *x, int n_blocks, int K, int8_t *qs, float *d, float *s, hipStream_t st)
 {
-    k_sort<<<1, SORT_THREADS, 0, st>>>(ids, wts, n_expert, k, T, dp);
+    if (n_blocks <= 0) return hipSuccess;
+    k_quant_rows<<<(n_blocks + 255) / 256, 256, 0, st>>>(x, n_blocks, K, qs, d, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const float *y, const Dispatch &dp, const float *glogit, int has_shared, int T, int P, int k,
+                          int E, float *out, int add, hipStream_t st)
+{
+    CombineArgs c{y, dp, glogit, out, T, P, k, E, has_shared, add};
+    dim3 grid((E + 255) / 256, T);
+    k_combine<<<grid, 256, 0, st>>>(c);
     return hipGetLastError();
 }
 
 hipError_t launch_gateup(const MvArgs &a, hipStream_t st) { return launch_mv<true>(a, st); }
 
 hipError_t launch_down(const MvArgs &a, hipStream_t st) { return launch_mv<false>(a, st); }
-
-hipError_t launch_combine(const float *y, const Dispatch &dp, const float *glogit, int has_shared, int T, int P,
-                          int k, int E, float *out, int add, hipStream_t st)
-{
-    dim3 grid((E + 255) / 256, T);
-    k_combine<<<grid, 256, 0, st>>>(y, dp, glogit, has_shared, T, P, k, E, out, add);
-    return hipGetLastError();
-}
 
 } // namespace biv

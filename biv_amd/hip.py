@@ -32,7 +32,7 @@ SYMBOLS = [
     "biv_hip_set_timing", "biv_hip_stage_times",
 ]
 
-STAGES = ["quant_h", "router", "route", "dispatch", "gate_up", "quant_act", "down", "combine"]
+STAGES = ["router", "route_sort", "gate_up", "quant_act", "down", "combine"]
 
 
 class HipError(RuntimeError):
