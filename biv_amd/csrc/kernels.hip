@@ -187,77 +187,106 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
 // the k highest probabilities with the lower expert first among equals, and
 // weights p / max(sum of the k in rank order, 1/16384).  One wavefront per
 // token, up to 8 logits per lane.
-__device__ inline bool better(float pa, int ia, float pb, int ib) { return pa > pb || (pa == pb && ia < ib); }
+constexpr int MAX_EXPERTS_PER_LANE = 4; // 256 experts over a wavefront
 
-__device__ void route_token(const float *__restrict__ logits, int n_expert, int k, int t, int *__restrict__ ids,
-                            float *__restrict__ wts)
+// f32 <-> unsigned with the same order (for finite values and infinities)
+__device__ inline unsigned f32_to_ordered(float x)
+{
+    const unsigned b = __float_as_uint(x);
+    return b & 0x80000000u ? ~b : b | 0x80000000u;
+}
+__device__ inline float ordered_to_f32(unsigned u) { return __uint_as_float(u & 0x80000000u ? u & 0x7FFFFFFFu : ~u); }
+
+// Max over the wavefront of an unsigned value, in every lane: DPP within
+// rows of 16 lanes, then the four row results through scalar registers.
+__device__ inline unsigned wave_max_u32(unsigned v)
+{
+    v = max(v, (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    v = max(v, (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    v = max(v, (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, false)); // row_ror:4
+    v = max(v, (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false)); // row_ror:8
+    const unsigned r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+    const unsigned r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
+// route (model.rs:256-268) of token t by one wavefront: softmax over the
+// logits (ops.rs:192-201), the k highest probabilities with the lower expert
+// first among equals, weights p / max(sum of the k in rank order, 1/16384).
+// `es` is this wave's LDS scratch of n_expert floats.  Ids and weights go to
+// ids/wts and, when given, to the LDS copies lds_ids/lds_wts.
+constexpr int RPER = MAX_EXPERTS_PER_LANE;
+
+__device__ void route_token(const float *__restrict__ logits, int n_expert, int k, int t, float *es,
+                            int *__restrict__ ids, float *__restrict__ wts, int *lds_ids, float *lds_wts)
 {
     const int lane = threadIdx.x & 63;
-    constexpr int PER = 8;
-    float v[PER];
+    float v[RPER];
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < PER; j++) {
-        int i = lane + WAVE * j;
+    for (int j = 0; j < RPER; j++) {
+        const int i = lane + WAVE * j;
         v[j] = i < n_expert ? logits[(size_t)t * n_expert + i] : -INFINITY;
         mx = fmaxf(mx, v[j]);
     }
+    if (mx != mx) mx = -INFINITY; // f32::max skips NaN
+    mx = ordered_to_f32(wave_max_u32(f32_to_ordered(mx)));
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        int i = lane + WAVE * j;
+    for (int j = 0; j < RPER; j++) {
+        const int i = lane + WAVE * j;
         v[j] = i < n_expert ? exp_f32(v[j] - mx) : 0.0f;
+        if (i < n_expert) es[i] = v[j];
     }
-    // the sum in index order, as the reference's loop adds it; every lane
-    // walks the same sequence (lanes past n_expert hold +0, which adds nothing)
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    // the sum in index order, as the reference's loop adds it: one chain, the
+    // same in every lane
     float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        if (WAVE * j >= n_expert) break;
-#pragma unroll
-        for (int ln = 0; ln < WAVE; ln++)
-            sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), ln));
+    const float4 *e4 = reinterpret_cast<const float4 *>(es);
+    for (int i = 0; i < n_expert / 4; i++) {
+        const float4 q = e4[i];
+        sum = sum + q.x;
+        sum = sum + q.y;
+        sum = sum + q.z;
+        sum = sum + q.w;
     }
+    for (int i = n_expert & ~3; i < n_expert; i++) sum = sum + es[i];
     const float inv = 1.0f / sum;
-    float p[PER];
-    unsigned taken = 0;
+    // probabilities as keys: bits + 1 orders like the float (p >= 0), 0 once taken
+    unsigned key[RPER];
 #pragma unroll
-    for (int j = 0; j < PER; j++) p[j] = v[j] * inv;
+    for (int j = 0; j < RPER; j++) key[j] = lane + WAVE * j < n_expert ? __float_as_uint(v[j] * inv) + 1u : 0u;
     float sel_p = 0.0f, s = 0.0f;
     int sel_i = 0;
     for (int r = 0; r < k; r++) {
-        float bp = -1.0f;
-        int bi = 0x7fffffff;
+        unsigned best = 0;
 #pragma unroll
-        for (int j = 0; j < PER; j++) {
-            int i = lane + WAVE * j;
-            if (i < n_expert && !(taken >> j & 1) && better(p[j], i, bp, bi)) {
-                bp = p[j];
-                bi = i;
-            }
-        }
+        for (int j = 0; j < RPER; j++) best = max(best, key[j]);
+        best = wave_max_u32(best);
+        // the lowest index holding it: first row j, lowest lane
+        int bi = -1;
 #pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            float op = __shfl_xor(bp, m);
-            int oi = __shfl_xor(bi, m);
-            if (better(op, oi, bp, bi)) {
-                bp = op;
-                bi = oi;
-            }
+        for (int j = 0; j < RPER; j++) {
+            const unsigned long long m = __ballot(key[j] == best && best != 0);
+            if (bi < 0 && m) bi = WAVE * j + __ffsll((long long)m) - 1;
         }
-        // NaN probabilities (non-finite h) match no candidate: take the lowest
-        // free expert so that ids stay in range
-        if (bi >= n_expert) {
-            int j = 0;
-            for (; j < n_expert; j++) {
-                const int owner_taken = __shfl((int)taken, j & 63);
-                if (!((owner_taken >> (j >> 6)) & 1)) break;
+        float bp;
+        if (bi < 0) {
+            // NaN probabilities (non-finite h) give no candidate: the lowest
+            // expert not yet chosen keeps the ids in range
+            bi = 0;
+#pragma unroll
+            for (int j = RPER - 1; j >= 0; j--) {
+                const unsigned long long m = __ballot(lane + WAVE * j < n_expert && key[j] != 0);
+                if (m) bi = WAVE * j + __ffsll((long long)m) - 1;
             }
-            bi = j < n_expert ? j : 0;
             bp = 0.0f;
+        } else {
+            bp = __uint_as_float(best - 1u);
         }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+#pragma unroll
+        for (int j = 0; j < RPER; j++)
+            if (lane + WAVE * j == bi) key[j] = 0;
         if (r == lane) {
             sel_p = bp;
             sel_i = bi;
@@ -266,8 +295,13 @@ __device__ void route_token(const float *__restrict__ logits, int n_expert, int 
     }
     s = fmaxf(s, 1.0f / 16384.0f);
     if (lane < k) {
+        const float w = sel_p / s;
         ids[(size_t)t * k + lane] = sel_i;
-        wts[(size_t)t * k + lane] = sel_p / s;
+        wts[(size_t)t * k + lane] = w;
+        if (lds_ids) {
+            lds_ids[t * k + lane] = sel_i;
+            lds_wts[t * k + lane] = w;
+        }
     }
 }
 
@@ -279,23 +313,26 @@ __device__ void route_token(const float *__restrict__ logits, int n_expert, int 
 // the number of earlier tokens with that expert, read from a token bitmap, so
 // the order is deterministic.  Run by one workgroup of NT threads.
 constexpr int MAX_EXPERTS = 256;
-constexpr int RS_THREADS = 256;
+constexpr int RS_THREADS = 1024;
 
-// Inclusive scan of v over the MAX_EXPERTS first threads (all threads call it).
+// Inclusive scan of v over the MAX_EXPERTS first threads (all threads call
+// it): a shuffle scan in each of the first four wavefronts, then the wave
+// totals through LDS.
 template <int NT> __device__ inline int scan_experts(int v, int *buf)
 {
-    const int tid = threadIdx.x;
-    if (tid < MAX_EXPERTS) buf[tid] = v;
-    __syncthreads();
-    for (int off = 1; off < MAX_EXPERTS; off <<= 1) {
-        int add = (tid < MAX_EXPERTS && tid >= off) ? buf[tid - off] : 0;
-        __syncthreads();
-        if (tid < MAX_EXPERTS) buf[tid] += add;
-        __syncthreads();
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    int x = tid < MAX_EXPERTS ? v : 0;
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+        const int y = __shfl_up(x, off);
+        if (lane >= off) x += y;
     }
-    const int r = tid < MAX_EXPERTS ? buf[tid] : 0;
+    if (tid < MAX_EXPERTS && lane == WAVE - 1) buf[w] = x;
     __syncthreads();
-    return r;
+    int add = 0;
+    for (int i = 0; i < w && i < MAX_EXPERTS / WAVE; i++) add += buf[i];
+    __syncthreads();
+    return tid < MAX_EXPERTS ? x + add : 0;
 }
 
 template <int NT>
@@ -309,11 +346,13 @@ __device__ void sort_pairs(const int *__restrict__ ids, const float *__restrict_
     __shared__ unsigned bm[MAX_EXPERTS][NT / 32];
     const int tid = threadIdx.x;
     const int P = T * k;
+    // the token bitmap needs ceil(min(T, NT) / 32) words per expert
+    const int nw_max = (min(T, NT) + 31) / 32;
     for (int e = tid; e < MAX_EXPERTS; e += NT) {
         cnt[e] = 0;
         run[e] = 0;
     }
-    for (int i = tid; i < MAX_EXPERTS * (NT / 32); i += NT) (&bm[0][0])[i] = 0u;
+    for (int i = tid; i < MAX_EXPERTS * nw_max; i += NT) bm[i / nw_max][i % nw_max] = 0u;
     __syncthreads();
     for (int i = tid; i < P; i += NT) atomicAdd(&cnt[ids[i]], 1); // ids < n_expert (route_token)
     __syncthreads();
@@ -342,32 +381,25 @@ __device__ void sort_pairs(const int *__restrict__ ids, const float *__restrict_
             for (int j = 0; j < k; j++) atomicOr(&bm[ids[(size_t)t * k + j]][word], bit);
         __syncthreads();
         if (t < T) {
-            int pos[16];
             for (int j = 0; j < k; j++) {
-                int e = ids[(size_t)t * k + j];
+                const int e = ids[(size_t)t * k + j];
                 int r = run[e] + __popc(bm[e][word] & (bit - 1));
                 for (int w = 0; w < word; w++) r += __popc(bm[e][w]);
-                int p = cnt[e] + r;
+                const int p = cnt[e] + r;
                 dp.pair_tok[p] = t;
                 dp.pair_exp[p] = e;
                 dp.pair_w[p] = wts[(size_t)t * k + j];
-                pos[j] = p;
+                // positions ascend with the expert id: the pair's place among
+                // the token's k is the number of its experts below e
+                int rank = 0;
+                for (int j2 = 0; j2 < k; j2++) rank += ids[(size_t)t * k + j2] < e;
+                dp.tok_pairs[(size_t)t * k + rank] = p;
             }
-            // positions ascend with the expert id: insertion sort of k values
-            for (int a = 1; a < k; a++) {
-                int v = pos[a], b = a - 1;
-                while (b >= 0 && pos[b] > v) {
-                    pos[b + 1] = pos[b];
-                    b--;
-                }
-                pos[b + 1] = v;
-            }
-            for (int j = 0; j < k; j++) dp.tok_pairs[(size_t)t * k + j] = pos[j];
         }
         __syncthreads();
         if (tid < MAX_EXPERTS) {
             int add = 0;
-            for (int w = 0; w < NT / 32; w++) {
+            for (int w = 0; w < nw_max; w++) {
                 add += __popc(bm[tid][w]);
                 bm[tid][w] = 0u;
             }
@@ -377,12 +409,27 @@ __device__ void sort_pairs(const int *__restrict__ ids, const float *__restrict_
     }
 }
 
-// One wavefront per token routes it; the workgroup that finishes last sorts.
+// One wavefront per token routes it, then one workgroup sorts: with a single
+// workgroup (T <= RS_WAVES) from LDS, else the workgroup that finishes
+// routing last, from global memory.
+constexpr int RS_WAVES = RS_THREADS / WAVE;
+
 __global__ __launch_bounds__(RS_THREADS) void k_route_sort(const float *__restrict__ logits, int n_expert, int k,
                                                            int T, int chunk, Dispatch dp, int *counter)
 {
-    const int t = blockIdx.x * (RS_THREADS / WAVE) + (threadIdx.x >> 6);
-    if (t < T) route_token(logits, n_expert, k, t, dp.ids, dp.wts);
+    __shared__ float es[RS_WAVES][MAX_EXPERTS];
+    __shared__ int lds_ids[RS_WAVES * 16];
+    __shared__ float lds_wts[RS_WAVES * 16];
+    const int wave = threadIdx.x >> 6;
+    const bool single = gridDim.x == 1;
+    for (int t = blockIdx.x * RS_WAVES + wave; t < T; t += gridDim.x * RS_WAVES)
+        route_token(logits, n_expert, k, t, es[wave], dp.ids, dp.wts, single ? lds_ids : nullptr,
+                    single ? lds_wts : nullptr);
+    if (single) {
+        __syncthreads();
+        sort_pairs<RS_THREADS>(lds_ids, lds_wts, n_expert, k, T, chunk, dp);
+        return;
+    }
     if (!finishing_workgroup(counter, gridDim.x)) return;
     sort_pairs<RS_THREADS>(dp.ids, dp.wts, n_expert, k, T, chunk, dp);
 }
@@ -749,8 +796,9 @@ hipError_t launch_router(const RouterArgs &a, hipStream_t st)
 hipError_t launch_route_sort(const float *logits, int n_expert, int k, int T, int chunk, const Dispatch &dp,
                              int *counter, hipStream_t st)
 {
-    k_route_sort<<<(T + RS_THREADS / WAVE - 1) / (RS_THREADS / WAVE), RS_THREADS, 0, st>>>(logits, n_expert, k, T,
-                                                                                           chunk, dp, counter);
+    // a single workgroup routes and sorts in LDS while every token has its wavefront
+    const int groups = T <= RS_WAVES ? 1 : (T + RS_WAVES - 1) / RS_WAVES;
+    k_route_sort<<<groups, RS_THREADS, 0, st>>>(logits, n_expert, k, T, chunk, dp, counter);
     return hipGetLastError();
 }
 
