@@ -340,19 +340,19 @@ __device__ void sort_pairs(const int *__restrict__ ids, const float *__restrict_
                            int chunk, const Dispatch &dp)
 {
     static_assert(NT >= MAX_EXPERTS, "one thread per expert");
+    constexpr int TPC_MAX = NT < 256 ? NT : 256; // tokens placed per round
     __shared__ int cnt[MAX_EXPERTS];
     __shared__ int scan[MAX_EXPERTS];
     __shared__ int run[MAX_EXPERTS];
-    __shared__ unsigned bm[MAX_EXPERTS][NT / 32];
+    __shared__ unsigned bm[MAX_EXPERTS][TPC_MAX / 32];
+    __shared__ int sid[NT];
+    __shared__ float sw[NT];
     const int tid = threadIdx.x;
     const int P = T * k;
-    // the token bitmap needs ceil(min(T, NT) / 32) words per expert
-    const int nw_max = (min(T, NT) + 31) / 32;
     for (int e = tid; e < MAX_EXPERTS; e += NT) {
         cnt[e] = 0;
         run[e] = 0;
     }
-    for (int i = tid; i < MAX_EXPERTS * nw_max; i += NT) bm[i / nw_max][i % nw_max] = 0u;
     __syncthreads();
     for (int i = tid; i < P; i += NT) atomicAdd(&cnt[ids[i]], 1); // ids < n_expert (route_token)
     __syncthreads();
@@ -372,37 +372,45 @@ __device__ void sort_pairs(const int *__restrict__ ids, const float *__restrict_
         cnt[tid] = beg; // from here on: the expert's first position
     }
     if (tid == MAX_EXPERTS - 1) *dp.n_slots = sl_incl;
-    __syncthreads();
-    for (int c0 = 0; c0 < T; c0 += NT) {
-        const int t = c0 + tid;
-        const int word = tid >> 5;
-        const unsigned bit = 1u << (tid & 31);
-        if (t < T)
-            for (int j = 0; j < k; j++) atomicOr(&bm[ids[(size_t)t * k + j]][word], bit);
+    // place the pairs, tpc tokens at a time, one thread per pair: a pair's
+    // place among its expert's pairs is `run` (earlier rounds) plus the
+    // earlier tokens of this round with that expert, read from a bitmap
+    const int tpc = min(NT / k, TPC_MAX);
+    const int nw = (tpc + 31) / 32;
+    for (int t0 = 0; t0 < T; t0 += tpc) {
+        const int nt = min(tpc, T - t0), np = nt * k;
+        for (int i = tid; i < np; i += NT) {
+            sid[i] = ids[(size_t)t0 * k + i];
+            sw[i] = wts[(size_t)t0 * k + i];
+        }
+        for (int i = tid; i < MAX_EXPERTS * nw; i += NT) bm[i / nw][i % nw] = 0u;
         __syncthreads();
-        if (t < T) {
-            for (int j = 0; j < k; j++) {
-                const int e = ids[(size_t)t * k + j];
-                int r = run[e] + __popc(bm[e][word] & (bit - 1));
-                for (int w = 0; w < word; w++) r += __popc(bm[e][w]);
-                const int p = cnt[e] + r;
-                dp.pair_tok[p] = t;
-                dp.pair_exp[p] = e;
-                dp.pair_w[p] = wts[(size_t)t * k + j];
-                // positions ascend with the expert id: the pair's place among
-                // the token's k is the number of its experts below e
-                int rank = 0;
-                for (int j2 = 0; j2 < k; j2++) rank += ids[(size_t)t * k + j2] < e;
-                dp.tok_pairs[(size_t)t * k + rank] = p;
-            }
+        const int tl = tid / k;
+        const unsigned bit = 1u << (tl & 31);
+        int e = 0;
+        if (tid < np) {
+            e = sid[tid];
+            atomicOr(&bm[e][tl >> 5], bit);
+        }
+        __syncthreads();
+        if (tid < np) {
+            int r = run[e] + __popc(bm[e][tl >> 5] & (bit - 1));
+            for (int w = 0; w < (tl >> 5); w++) r += __popc(bm[e][w]);
+            const int p = cnt[e] + r;
+            const int t = t0 + tl;
+            dp.pair_tok[p] = t;
+            dp.pair_exp[p] = e;
+            dp.pair_w[p] = sw[tid];
+            // positions ascend with the expert id: the pair's place among the
+            // token's k is the number of its experts below e
+            int rank = 0;
+            for (int j2 = 0; j2 < k; j2++) rank += sid[tl * k + j2] < e;
+            dp.tok_pairs[(size_t)t * k + rank] = p;
         }
         __syncthreads();
         if (tid < MAX_EXPERTS) {
             int add = 0;
-            for (int w = 0; w < nw_max; w++) {
-                add += __popc(bm[tid][w]);
-                bm[tid][w] = 0u;
-            }
+            for (int w = 0; w < nw; w++) add += __popc(bm[tid][w]);
             run[tid] += add;
         }
         __syncthreads();
@@ -633,6 +641,7 @@ struct CombineArgs {
 // has its own row.  The weight row is loaded once and met by every token of
 // the expert.
 constexpr int MV_WAVES = 4;
+constexpr int XT = 8; // activation rows staged in LDS at a time
 
 template <int TY, int K, bool GATEUP, bool DUMP>
 __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
@@ -663,16 +672,45 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
     Chain<TY, K> wc;
     wc.load(M, mrow, pi, l);
     int32_t *dump = DUMP ? (m ? a.dump_b : a.dump_a) : nullptr;
-    for (int i = 0; i < cnt; i++) {
+    // the slot's activation rows, XT at a time, staged in LDS by the whole
+    // workgroup: every group of every wave reads them from there
+    __shared__ int4 sx[XT][K / 16];
+    __shared__ float4 sd[XT][K / 128];
+    constexpr int ROW16 = K / 16 + K / 128; // 16-byte pieces of a staged row
+    for (int i0 = 0; i0 < cnt; i0 += XT) {
+        const int nt = min(XT, cnt - i0);
+        for (int idx = threadIdx.x; idx < nt * ROW16; idx += blockDim.x) {
+            const int j = idx / ROW16, r = idx % ROW16, i = i0 + j;
+            const size_t xrow =
+                a.x_by_token ? (size_t)(shared ? tok0 + i : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
+            if (r < K / 16) sx[j][r] = reinterpret_cast<const int4 *>(a.xq + xrow * K)[r];
+            else sd[j][r - K / 16] = reinterpret_cast<const float4 *>(a.xd + xrow * (K / 32))[r - K / 16];
+        }
+        __syncthreads();
+    for (int j = 0; j < nt; j++) {
+        const int i = i0 + j;
         const size_t xrow = a.x_by_token ? (size_t)(shared ? tok0 + i : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
         const size_t orow = (size_t)(beg + i);
-        XChain<K> xc;
-        xc.load(a.xq, a.xd, xrow, pi, l);
+        int xw[S];
+        float xd[S];
+#pragma unroll
+        for (int q = 0; q < S / 4; q++) {
+            const int4 v = sx[j][q * 16 + pi * 8 + l];
+            xw[4 * q] = v.x;
+            xw[4 * q + 1] = v.y;
+            xw[4 * q + 2] = v.z;
+            xw[4 * q + 3] = v.w;
+            const float4 f = sd[j][pi * (S / 4) + q];
+            xd[4 * q] = f.x;
+            xd[4 * q + 1] = f.y;
+            xd[4 * q + 2] = f.z;
+            xd[4 * q + 3] = f.w;
+        }
         float acc = 0.0f;
 #pragma unroll
         for (int s = 0; s < S; s++) {
-            const int p = wc.partial(s, xc.x[s]);
-            acc = fmaf((float)p, wc.wscale(s) * xc.d[s], acc);
+            const int p = wc.partial(s, xw[s]);
+            acc = fmaf((float)p, wc.wscale(s) * xd[s], acc);
             if (DUMP) {
                 // the block's int32 is the sum of its 8 lanes' partials
                 int bs = p;
@@ -697,6 +735,8 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
         } else {
             if (ln == 0 && row_ok) a.out[orow * rows + row] = t;
         }
+    }
+        __syncthreads();
     }
 }
 

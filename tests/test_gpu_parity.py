@@ -116,12 +116,14 @@ def full_parity(orc, engine, layer, moe, h, block_dots=True):
     return rel, t
 
 
-@pytest.mark.parametrize("T", [1, 2, 5, 9])
+@pytest.mark.parametrize("T", [1, 2, 5, 9, 64, 65, 100])
 def test_q8_small_layer(orc, engine, T):
+    """T <= 64 runs the three-launch decode kernels, T > 64 the six-launch
+    path with token-chunked slots; both must give the oracle's bits."""
     print(f"case q8 small T={T}", flush=True)
     layer, moe = layer_for(engine, seed=21, n_expert=32)
     h = synth.make_tokens(100 + T, T, offsets=True)
-    full_parity(orc, engine, layer, moe, h)
+    full_parity(orc, engine, layer, moe, h, block_dots=T <= 9)
 
 
 @pytest.mark.parametrize("T", [1, 5, 40])
