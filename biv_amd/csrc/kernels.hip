@@ -456,7 +456,7 @@ template <int TY, int K> struct Chain;
 template <int K> struct Chain<T_Q8_0, K> {
     static constexpr int S = K / 64;
     int w[S];
-    float ws[S];
+    int hw[S / 2]; // the f16 scales, two per register
     __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l)
     {
         const int4 *q = reinterpret_cast<const int4 *>(M.q + mrow * K);
@@ -468,16 +468,14 @@ template <int K> struct Chain<T_Q8_0, K> {
             w[4 * i + 2] = v.z;
             w[4 * i + 3] = v.w;
         }
-        int hw[S / 2];
         ld_words(M.s + 2 * (mrow * (K / 32) + pi * S), hw);
-#pragma unroll
-        for (int i = 0; i < S / 2; i++) {
-            ws[2 * i] = __half2float(__ushort_as_half((unsigned short)(hw[i] & 0xFFFF)));
-            ws[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)((unsigned)hw[i] >> 16)));
-        }
     }
     __device__ inline int partial(int s, int x) const { return dot4(w[s], x, 0); }
-    __device__ inline float wscale(int s) const { return ws[s]; }
+    __device__ inline float wscale(int s) const
+    {
+        const unsigned h = (unsigned)hw[s >> 1] >> (16 * (s & 1));
+        return __half2float(__ushort_as_half((unsigned short)(h & 0xFFFF)));
+    }
 };
 
 // Q4_K: dot_u8_i8 of the low (pi 0) or high (pi 1) nibbles; scale d * sc
@@ -641,13 +639,21 @@ struct CombineArgs {
 // has its own row.  The weight row is loaded once and met by every token of
 // the expert.
 constexpr int MV_WAVES = 4;
+#ifndef MV_NSET_LONG
+#define MV_NSET_LONG 1
+#endif
+#ifndef MV_NSET_SHORT
+#define MV_NSET_SHORT 2
+#endif
 constexpr int XT = 8; // activation rows staged in LDS at a time
 
-template <int TY, int K, bool GATEUP, bool DUMP>
+// Each wave holds NSET sets of rows (four groups each), all loaded before the
+// first token: more bytes in flight per wave.
+template <int TY, int K, bool GATEUP, bool DUMP, int NSET>
 __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
 {
     constexpr int S = K / 64;
-    constexpr int RPW = GATEUP ? 2 : 4; // rows per wave
+    constexpr int RPW = GATEUP ? 2 : 4; // rows per set of a wave
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane >> 4, ln = lane & 15, pi = ln >> 3, l = ln & 7;
     const int u = blockIdx.y;
@@ -666,11 +672,13 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
     const int m = GATEUP ? (grp & 1) : 0;
     const DevMat &M = GATEUP && m ? (shared ? a.sb : a.b) : (shared ? a.sa : a.a);
     const int rows = M.rows;
-    const int row = (blockIdx.x * MV_WAVES + wave) * RPW + (GATEUP ? grp >> 1 : grp);
-    const bool row_ok = row < rows;
-    const size_t mrow = (size_t)e * rows + (row_ok ? row : 0);
-    Chain<TY, K> wc;
-    wc.load(M, mrow, pi, l);
+    const int row0 = (blockIdx.x * MV_WAVES + wave) * RPW * NSET + (GATEUP ? grp >> 1 : grp);
+    Chain<TY, K> wc[NSET];
+#pragma unroll
+    for (int q = 0; q < NSET; q++) {
+        const int row = row0 + q * RPW;
+        wc[q].load(M, (size_t)e * rows + (row < rows ? row : 0), pi, l);
+    }
     int32_t *dump = DUMP ? (m ? a.dump_b : a.dump_a) : nullptr;
     // the slot's activation rows, XT at a time, staged in LDS by the whole
     // workgroup: every group of every wave reads them from there
@@ -687,55 +695,61 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
             else sd[j][r - K / 16] = reinterpret_cast<const float4 *>(a.xd + xrow * (K / 32))[r - K / 16];
         }
         __syncthreads();
-    for (int j = 0; j < nt; j++) {
-        const int i = i0 + j;
-        const size_t xrow = a.x_by_token ? (size_t)(shared ? tok0 + i : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
-        const size_t orow = (size_t)(beg + i);
-        int xw[S];
-        float xd[S];
+        for (int j = 0; j < nt; j++) {
+            const int i = i0 + j;
+            const size_t xrow =
+                a.x_by_token ? (size_t)(shared ? tok0 + i : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
+            const size_t orow = (size_t)(beg + i);
+            int xw[S];
+            float xd[S];
 #pragma unroll
-        for (int q = 0; q < S / 4; q++) {
-            const int4 v = sx[j][q * 16 + pi * 8 + l];
-            xw[4 * q] = v.x;
-            xw[4 * q + 1] = v.y;
-            xw[4 * q + 2] = v.z;
-            xw[4 * q + 3] = v.w;
-            const float4 f = sd[j][pi * (S / 4) + q];
-            xd[4 * q] = f.x;
-            xd[4 * q + 1] = f.y;
-            xd[4 * q + 2] = f.z;
-            xd[4 * q + 3] = f.w;
-        }
-        float acc = 0.0f;
+            for (int q = 0; q < S / 4; q++) {
+                const int4 v = sx[j][q * 16 + pi * 8 + l];
+                xw[4 * q] = v.x;
+                xw[4 * q + 1] = v.y;
+                xw[4 * q + 2] = v.z;
+                xw[4 * q + 3] = v.w;
+                const float4 f = sd[j][pi * (S / 4) + q];
+                xd[4 * q] = f.x;
+                xd[4 * q + 1] = f.y;
+                xd[4 * q + 2] = f.z;
+                xd[4 * q + 3] = f.w;
+            }
 #pragma unroll
-        for (int s = 0; s < S; s++) {
-            const int p = wc.partial(s, xw[s]);
-            acc = fmaf((float)p, wc.wscale(s) * xd[s], acc);
-            if (DUMP) {
-                // the block's int32 is the sum of its 8 lanes' partials
-                int bs = p;
-                bs += __shfl_xor(bs, 1);
-                bs += __shfl_xor(bs, 2);
-                bs += __shfl_xor(bs, 4);
-                if (dump && l == 0 && row_ok) dump[(orow * rows + row) * (K / 32) + 2 * s + pi] = bs;
+            for (int q = 0; q < NSET; q++) {
+                const int row = row0 + q * RPW;
+                const bool row_ok = row < rows;
+                float acc = 0.0f;
+#pragma unroll
+                for (int s = 0; s < S; s++) {
+                    const int p = wc[q].partial(s, xw[s]);
+                    acc = fmaf((float)p, wc[q].wscale(s) * xd[s], acc);
+                    if (DUMP) {
+                        // the block's int32 is the sum of its 8 lanes' partials
+                        int bs = p;
+                        bs += __shfl_xor(bs, 1);
+                        bs += __shfl_xor(bs, 2);
+                        bs += __shfl_xor(bs, 4);
+                        if (dump && l == 0 && row_ok) dump[(orow * rows + row) * (K / 32) + 2 * s + pi] = bs;
+                    }
+                }
+                float t = acc + __shfl_xor(acc, 8); // acc0 + acc1, lane by lane
+                t = t + __shfl_xor(t, 4);           // the two 128-bit halves
+                t = t + __shfl_xor(t, 2);           // movehl
+                t = t + __shfl_xor(t, 1);           // movehdup
+                if (TY == T_Q4K) {
+                    float mins = 0.0f;
+                    if (ln == 0) mins = q4k_mins<K>(M, (size_t)e * rows + (row_ok ? row : 0), a.xs, xrow);
+                    t = t - __shfl(mins, lane & ~15);
+                }
+                if (GATEUP) {
+                    const float up = __shfl_xor(t, 16);
+                    if (m == 0 && ln == 0 && row_ok) a.out[orow * rows + row] = silu_mul(t, up);
+                } else {
+                    if (ln == 0 && row_ok) a.out[orow * rows + row] = t;
+                }
             }
         }
-        float t = acc + __shfl_xor(acc, 8); // acc0 + acc1, lane by lane
-        t = t + __shfl_xor(t, 4);           // the two 128-bit halves
-        t = t + __shfl_xor(t, 2);           // movehl
-        t = t + __shfl_xor(t, 1);           // movehdup
-        if (TY == T_Q4K) {
-            float mins = 0.0f;
-            if (ln == 0) mins = q4k_mins<K>(M, mrow, a.xs, xrow);
-            t = t - __shfl(mins, lane & ~15);
-        }
-        if (GATEUP) {
-            const float up = __shfl_xor(t, 16);
-            if (m == 0 && ln == 0 && row_ok) a.out[orow * rows + row] = silu_mul(t, up);
-        } else {
-            if (ln == 0 && row_ok) a.out[orow * rows + row] = t;
-        }
-    }
         __syncthreads();
     }
 }
@@ -776,12 +790,14 @@ hipError_t launch_mv_t(MvArgs a, int routed, int shared, hipStream_t st)
     if (!routed) a.u_max = 0; // the slots are the shared expert's
     const int slots = (routed ? a.u_max : 0) + (shared ? (a.T + a.chunk - 1) / a.chunk : 0);
     if (slots == 0) return hipSuccess;
-    const int rows_per_wg = MV_WAVES * (GATEUP ? 2 : 4);
-    dim3 grid((M.rows + rows_per_wg - 1) / rows_per_wg, slots);
     dim3 block(MV_WAVES * WAVE);
+    // row sets per wave: the shorter the rows, the more of them in flight
 #define BIV_MV_CASE(TY, KK)                                                                                     \
     if (M.ty == TY && M.cols == KK) {                                                                           \
-        k_chain_mv<TY, KK, GATEUP, DUMP><<<grid, block, 0, st>>>(a);                                            \
+        constexpr int NSET = KK >= 2048 ? MV_NSET_LONG : MV_NSET_SHORT;                                         \
+        const int rows_per_wg = MV_WAVES * (GATEUP ? 2 : 4) * NSET;                                             \
+        dim3 grid((M.rows + rows_per_wg - 1) / rows_per_wg, slots);                                             \
+        k_chain_mv<TY, KK, GATEUP, DUMP, NSET><<<grid, block, 0, st>>>(a);                                      \
         return hipGetLastError();                                                                               \
     }
     BIV_MV_CASE(T_Q8_0, 2048)
