@@ -268,10 +268,7 @@ int scratch_fit(biv_hip_ctx *ctx, const biv_hip_moe *m, int T)
     rc = rc ? rc : sc_alloc(ctx, R * E, &s.y);
     rc = rc ? rc : sc_alloc(ctx, cap * E, &s.h_stage);
     rc = rc ? rc : sc_alloc(ctx, cap * E, &s.o_stage);
-    rc = rc ? rc : sc_alloc(ctx, 1, &s.dp.n_slots);
-    rc = rc ? rc : sc_alloc(ctx, ne + P, &s.dp.sl_expert);
-    rc = rc ? rc : sc_alloc(ctx, ne + P, &s.dp.sl_beg);
-    rc = rc ? rc : sc_alloc(ctx, ne + P, &s.dp.sl_cnt);
+    rc = rc ? rc : sc_alloc(ctx, ne + P, &s.dp.slots); // >= max_slots(ne, P, chunk)
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_tok);
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_exp);
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_w);
@@ -345,6 +342,7 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     // cut them so that hot experts and the shared expert spread over the GPU
     const int chunk = T <= 64 ? 64 : 16;
     const int u_max = biv::max_slots(ne, P, chunk);
+    s.dp.slot_cap = u_max;
 
     biv::RouterArgs ra{};
     ra.router = reinterpret_cast<const float *>(m->router->m.q);
@@ -381,7 +379,6 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     a.T = T;
     a.P = P;
     a.u_max = u_max;
-    a.chunk = chunk;
     a.x_by_token = 1;
     HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
     MARK();
@@ -401,7 +398,6 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     d.T = T;
     d.P = P;
     d.u_max = u_max;
-    d.chunk = chunk;
     d.x_by_token = 0;
     HIP_TRY(ctx, biv::launch_down(d, st), "expert down");
     MARK();

@@ -30,15 +30,22 @@ struct DevMat {
     uint8_t *d = nullptr;
 };
 
+// A run of at most `chunk` consecutive dispatch positions of one expert.
+// Consumers read the whole record with scalar loads; tok[] holds the tokens
+// of its first SLOT_TOKS pairs (entries past cnt are not written).
+constexpr int SLOT_TOKS = 8;
+struct alignas(16) Slot {
+    int expert, beg, cnt, pad; // cnt 0: an unused slot
+    int tok[SLOT_TOKS];
+};
+
 // Routing and dispatch state of one forward of T tokens (device pointers).
 // A slot is a run of at most `chunk` consecutive pairs of one expert; an
 // expert with more pairs has several slots.  Slots are in ascending expert
 // order.
 struct Dispatch {
-    int *n_slots;    // [1] slots of the routed experts
-    int *sl_expert;  // [max slots] expert of slot u
-    int *sl_beg;     // [max slots] first dispatch position of slot u
-    int *sl_cnt;     // [max slots] pairs of slot u (<= chunk)
+    struct Slot *slots; // [slot_cap]
+    int slot_cap;       // slots the consumers' grids cover (max_slots); the sort writes every one
     int *pair_tok;   // [P] token of each pair in dispatch order
     int *pair_exp;   // [P] expert of each pair in dispatch order
     float *pair_w;   // [P] routing weight of each pair
@@ -86,8 +93,9 @@ struct MvArgs {
     int32_t *dump_a;        // optional [P + T][rows][K/32] block int32 dots of a
     int32_t *dump_b;        // optional, of b
     int T, P;
-    int u_max;              // grid slots of the routed experts (max_slots); the shared expert's follow
-    int chunk;              // pairs per slot; the shared expert's T tokens are cut the same way
+    int u_max;              // grid slots of the routed experts (max_slots)
+    int n_sh;               // grid slots of the shared expert, which come first (set by the launcher)
+    int sh_chunk;           // tokens per shared-expert slot (set by the launcher)
     int x_by_token;         // 1: input row of a pair is its token's (gate/up); 0: the pair's own (down)
 };
 

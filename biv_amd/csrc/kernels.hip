@@ -361,17 +361,22 @@ __device__ void sort_pairs(const int *__restrict__ ids, const float *__restrict_
     const int nsl = (c + chunk - 1) / chunk;
     const int pos_incl = scan_experts<NT>(c, scan);
     const int sl_incl = scan_experts<NT>(nsl, scan);
+    __shared__ int n_used;
+    __shared__ int sfirst[MAX_EXPERTS];
     if (tid < n_expert) {
         const int beg = pos_incl - c;
         for (int j = 0; j < nsl; j++) {
-            const int u = sl_incl - nsl + j;
-            dp.sl_expert[u] = tid;
-            dp.sl_beg[u] = beg + j * chunk;
-            dp.sl_cnt[u] = min(chunk, c - j * chunk);
+            int4 *rec = reinterpret_cast<int4 *>(&dp.slots[sl_incl - nsl + j]);
+            rec[0] = make_int4(tid, beg + j * chunk, min(chunk, c - j * chunk), 0);
         }
         cnt[tid] = beg; // from here on: the expert's first position
+        sfirst[tid] = sl_incl - nsl;
     }
-    if (tid == MAX_EXPERTS - 1) *dp.n_slots = sl_incl;
+    if (tid == MAX_EXPERTS - 1) n_used = sl_incl;
+    __syncthreads();
+    // the slots past the used ones are empty, so that a consumer needs one record
+    for (int u = n_used + tid; u < dp.slot_cap; u += NT)
+        reinterpret_cast<int4 *>(&dp.slots[u])[0] = make_int4(0, 0, 0, 0);
     // place the pairs, tpc tokens at a time, one thread per pair: a pair's
     // place among its expert's pairs is `run` (earlier rounds) plus the
     // earlier tokens of this round with that expert, read from a bitmap
@@ -399,6 +404,7 @@ __device__ void sort_pairs(const int *__restrict__ ids, const float *__restrict_
             const int p = cnt[e] + r;
             const int t = t0 + tl;
             dp.pair_tok[p] = t;
+            if (r % chunk < SLOT_TOKS) dp.slots[sfirst[e] + r / chunk].tok[r % chunk] = t;
             dp.pair_exp[p] = e;
             dp.pair_w[p] = sw[tid];
             // positions ascend with the expert id: the pair's place among the
@@ -632,8 +638,9 @@ struct CombineArgs {
 };
 
 // ---------------------------------------------------------------------------
-// Grouped expert matvec.  blockIdx.y is an active-expert slot (or, at u_max,
-// the shared expert).  A wave is four 16-lane groups; a group runs the 16
+// Grouped expert matvec.  blockIdx.y is a slot: first the shared expert's
+// (its tokens in runs of XT, dispatched first as they are the longest-running
+// workgroups when T is large), then the routed experts'.  A wave is four 16-lane groups; a group runs the 16
 // chains of one (matrix, row): for gate/up, groups (row, gate) and (row, up)
 // sit side by side and the SwiGLU is formed in registers; for down each group
 // has its own row.  The weight row is loaded once and met by every token of
@@ -657,22 +664,74 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane >> 4, ln = lane & 15, pi = ln >> 3, l = ln & 7;
     const int u = blockIdx.y;
-    const bool shared = u >= a.u_max;
+    const bool shared = u < a.n_sh;
     int e = 0, beg, cnt, tok0 = 0;
+    Slot sl;
     if (shared) {
-        tok0 = (u - a.u_max) * a.chunk; // the shared expert's tokens [tok0, tok0 + cnt)
+        tok0 = u * a.sh_chunk; // the shared expert's tokens [tok0, tok0 + cnt)
         beg = a.P + tok0;
-        cnt = min(a.chunk, a.T - tok0);
+        cnt = min(a.sh_chunk, a.T - tok0);
     } else {
-        if (u >= *a.dp.n_slots) return; // uniform over the workgroup
-        e = a.dp.sl_expert[u];
-        beg = a.dp.sl_beg[u];
-        cnt = a.dp.sl_cnt[u];
+        sl = a.dp.slots[u - a.n_sh];
+        if (sl.cnt == 0) return; // uniform over the workgroup
+        e = sl.expert;
+        beg = sl.beg;
+        cnt = sl.cnt;
     }
     const int m = GATEUP ? (grp & 1) : 0;
-    const DevMat &M = GATEUP && m ? (shared ? a.sb : a.b) : (shared ? a.sa : a.a);
+    // The group's matrix: the up matrix is addressed as the gate matrix plus
+    // a uniform byte offset, so that each plane is one pointer in scalar
+    // registers with a per-lane offset (a pointer chosen per lane would be
+    // read from the kernel arguments with vector loads, before any weight).
+    DevMat M = shared ? a.sa : a.a;
+    if (GATEUP && m) {
+        const DevMat &B = shared ? a.sb : a.b;
+        M.q += B.q - M.q;
+        M.s += B.s - M.s;
+        M.d += B.d - M.d;
+    }
     const int rows = M.rows;
     const int row0 = (blockIdx.x * MV_WAVES + wave) * RPW * NSET + (GATEUP ? grp >> 1 : grp);
+    // The slot's activation rows, XT at a time, staged in LDS by the whole
+    // workgroup (every group of every wave reads them from there), loaded
+    // straight from global memory into LDS.  Row j of a chunk is ROW16
+    // 16-byte pieces: its K/16 quant pieces, then its K/128 scale pieces.
+    constexpr int ROW16 = K / 16 + K / 128;
+    constexpr int NTH = MV_WAVES * WAVE;
+    constexpr int NPC = (XT * ROW16 + NTH - 1) / NTH; // pieces per thread
+    __shared__ int4 stage[NPC * NTH];
+    // piece idx of the chunk at i0 (nt rows; xr: its row in xq / xd) lands in stage[idx]
+    auto stage_piece = [&](int c, int idx, int xr) {
+        const int r = idx % ROW16;
+        const uint8_t *src = r < K / 16 ? reinterpret_cast<const uint8_t *>(a.xq) + (size_t)xr * K + 16 * r
+                                        : reinterpret_cast<const uint8_t *>(a.xd) + (size_t)xr * (K / 8) + 16 * (r - K / 16);
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)&stage[c * NTH + wave * WAVE], 16,
+                                         0, 0);
+    };
+    // The first chunk's loads go out before the weights': loads complete in
+    // order, so a gather issued after the weight loads would start only once
+    // the weights are in.  Its row numbers are in the slot record (scalar
+    // loads, which do not wait on vector loads).  Pieces past the chunk
+    // reread a valid row into unused LDS.
+    {
+        const int nt = min(XT, cnt);
+        int trow[XT];
+#pragma unroll
+        for (int j = 0; j < XT; j++) {
+            const int i = min(j, cnt - 1);
+            trow[j] = a.x_by_token ? (shared ? tok0 + i : (j < cnt ? sl.tok[j] : sl.tok[0])) : beg + i;
+        }
+#pragma unroll
+        for (int c = 0; c < NPC; c++) {
+            if (c * NTH >= nt * ROW16) break; // uniform
+            const int idx0 = (int)threadIdx.x + c * NTH, idx = idx0 < nt * ROW16 ? idx0 : nt * ROW16 - 1;
+            const int j = idx / ROW16;
+            int xr = trow[0];
+#pragma unroll
+            for (int jj = 1; jj < XT; jj++) xr = j == jj ? trow[jj] : xr;
+            stage_piece(c, idx, xr);
+        }
+    }
     Chain<TY, K> wc[NSET];
 #pragma unroll
     for (int q = 0; q < NSET; q++) {
@@ -680,19 +739,16 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
         wc[q].load(M, (size_t)e * rows + (row < rows ? row : 0), pi, l);
     }
     int32_t *dump = DUMP ? (m ? a.dump_b : a.dump_a) : nullptr;
-    // the slot's activation rows, XT at a time, staged in LDS by the whole
-    // workgroup: every group of every wave reads them from there
-    __shared__ int4 sx[XT][K / 16];
-    __shared__ float4 sd[XT][K / 128];
-    constexpr int ROW16 = K / 16 + K / 128; // 16-byte pieces of a staged row
     for (int i0 = 0; i0 < cnt; i0 += XT) {
         const int nt = min(XT, cnt - i0);
-        for (int idx = threadIdx.x; idx < nt * ROW16; idx += blockDim.x) {
-            const int j = idx / ROW16, r = idx % ROW16, i = i0 + j;
-            const size_t xrow =
-                a.x_by_token ? (size_t)(shared ? tok0 + i : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
-            if (r < K / 16) sx[j][r] = reinterpret_cast<const int4 *>(a.xq + xrow * K)[r];
-            else sd[j][r - K / 16] = reinterpret_cast<const float4 *>(a.xd + xrow * (K / 32))[r - K / 16];
+        if (i0 > 0) { // the first chunk is on its way
+#pragma unroll
+            for (int c = 0; c < NPC; c++) {
+                if (c * NTH >= nt * ROW16) break;
+                const int idx0 = (int)threadIdx.x + c * NTH, idx = idx0 < nt * ROW16 ? idx0 : nt * ROW16 - 1;
+                const int i = i0 + idx / ROW16;
+                stage_piece(c, idx, a.x_by_token ? (shared ? tok0 + i : a.dp.pair_tok[beg + i]) : beg + i);
+            }
         }
         __syncthreads();
         for (int j = 0; j < nt; j++) {
@@ -704,12 +760,12 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
             float xd[S];
 #pragma unroll
             for (int q = 0; q < S / 4; q++) {
-                const int4 v = sx[j][q * 16 + pi * 8 + l];
+                const int4 v = stage[j * ROW16 + q * 16 + pi * 8 + l];
                 xw[4 * q] = v.x;
                 xw[4 * q + 1] = v.y;
                 xw[4 * q + 2] = v.z;
                 xw[4 * q + 3] = v.w;
-                const float4 f = sd[j][pi * (S / 4) + q];
+                const float4 f = *reinterpret_cast<const float4 *>(&stage[j * ROW16 + K / 16 + pi * (S / 4) + q]);
                 xd[4 * q] = f.x;
                 xd[4 * q + 1] = f.y;
                 xd[4 * q + 2] = f.z;
@@ -787,8 +843,10 @@ template <bool GATEUP, bool DUMP>
 hipError_t launch_mv_t(MvArgs a, int routed, int shared, hipStream_t st)
 {
     const DevMat &M = routed ? a.a : a.sa;
-    if (!routed) a.u_max = 0; // the slots are the shared expert's
-    const int slots = (routed ? a.u_max : 0) + (shared ? (a.T + a.chunk - 1) / a.chunk : 0);
+    if (!routed) a.u_max = 0;
+    a.sh_chunk = XT;
+    a.n_sh = shared ? (a.T + XT - 1) / XT : 0;
+    const int slots = a.u_max + a.n_sh;
     if (slots == 0) return hipSuccess;
     dim3 block(MV_WAVES * WAVE);
     // row sets per wave: the shorter the rows, the more of them in flight
