@@ -291,6 +291,7 @@ int scratch_fit(biv_hip_ctx *ctx, const biv_hip_moe *m, int T)
 
 struct Dumps {
     int32_t *gate = nullptr, *up = nullptr, *down = nullptr;
+    bool act = false; // the quantised intermediate is read back
 };
 
 constexpr int N_STAGES = 6; // router (+ quantise h), route + dispatch, gate/up, quantise act, down, combine
@@ -383,7 +384,14 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
     MARK();
     const int rows_act = has_shared ? P + T : P;
-    HIP_TRY(ctx, biv::launch_quant_rows(s.act, rows_act * ff / 32, ff, s.aq, s.ad, s.as, st), "quantise act");
+    // For small T the down kernel quantises its rows itself, saving a launch
+    // (every workgroup of a slot quantises the slot's rows: past a few tokens
+    // that costs more than it saves), unless a down matrix is Q4_K, whose
+    // mins need the block sums.  The taps still want the rows apart.
+    const bool fused_quant =
+        T <= 16 && m->down->m.ty != biv::T_Q4K && (!has_shared || m->sd->m.ty != biv::T_Q4K);
+    if (!fused_quant || dm.act)
+        HIP_TRY(ctx, biv::launch_quant_rows(s.act, rows_act * ff / 32, ff, s.aq, s.ad, s.as, st), "quantise act");
     MARK();
 
     biv::MvArgs d{};
@@ -392,6 +400,7 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     d.xq = s.aq;
     d.xd = s.ad;
     d.xs = s.as;
+    d.xf = fused_quant ? s.act : nullptr;
     d.dp = s.dp;
     d.out = s.y;
     d.dump_a = dm.down;
@@ -610,6 +619,7 @@ int biv_hip_moe_forward_taps(biv_hip_ctx *ctx, const biv_hip_moe *moe, const flo
     if (taps && taps->gate_idots) dm.gate = dev(sizeof(int32_t) * R * ff * (E / 32));
     if (taps && taps->up_idots) dm.up = dev(sizeof(int32_t) * R * ff * (E / 32));
     if (taps && taps->down_idots) dm.down = dev(sizeof(int32_t) * R * E * (ff / 32));
+    dm.act = taps && (taps->act_q || taps->act_d);
     rc = forward(ctx, moe, s.h_stage, n, s.o_stage, flags, dm);
     auto d2h = [&](void *dst, const void *src, size_t bytes) {
         if (!rc && dst && src) {

@@ -65,7 +65,9 @@ template <int N> __device__ inline void ld_words(const void *p, int (&out)[N])
 // `row`: amax, d = amax / 127, id = 1/d (0 when d is 0), q =
 // round-half-away(v * id), s = d * sum(q); IEEE division and no contraction
 // keep it bit-exact.  Written in the chain layout (layout.hpp).
-__device__ inline void quant_block(const float (&v)[32], int K, size_t row, int b, int8_t *qs, float *d, float *s)
+// The row's quant words, block scales and block sums are at qrow, drow, srow
+// (srow may be null); generic pointers, so the row may be in LDS.
+__device__ inline void quant_block_at(const float (&v)[32], int K, int b, int *qrow, float *drow, float *srow)
 {
     float amax = 0.0f;
 #pragma unroll
@@ -73,7 +75,6 @@ __device__ inline void quant_block(const float (&v)[32], int K, size_t row, int 
     const float db = amax / 127.0f;
     const float id = db != 0.0f ? 1.0f / db : 0.0f;
     int sum = 0;
-    int *qrow = reinterpret_cast<int *>(qs + row * K);
 #pragma unroll
     for (int l = 0; l < 8; l++) {
         unsigned w = 0;
@@ -85,8 +86,39 @@ __device__ inline void quant_block(const float (&v)[32], int K, size_t row, int 
         }
         qrow[lay::q8_word(b, l)] = (int)w;
     }
-    d[row * (K / 32) + lay::q8_scale(K, b)] = db;
-    s[row * (K / 32) + lay::q8_scale(K, b)] = db * (float)sum;
+    drow[lay::q8_scale(K, b)] = db;
+    if (srow) srow[lay::q8_scale(K, b)] = db * (float)sum;
+}
+
+// The same from a block in LDS, read twice (amax, then the quants) so that
+// few registers are live.
+__device__ inline void quant_block_lds(const float4 *v, int K, int b, int *qrow, float *drow)
+{
+    float amax = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const float4 f = v[q];
+        amax = fmaxf(amax, fabsf(f.x));
+        amax = fmaxf(amax, fabsf(f.y));
+        amax = fmaxf(amax, fabsf(f.z));
+        amax = fmaxf(amax, fabsf(f.w));
+    }
+    const float db = amax / 127.0f;
+    const float id = db != 0.0f ? 1.0f / db : 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; l++) {
+        const float4 f = v[l];
+        const unsigned w = ((unsigned)((int)roundf(f.x * id)) & 0xFF) | (((unsigned)((int)roundf(f.y * id)) & 0xFF) << 8) |
+                           (((unsigned)((int)roundf(f.z * id)) & 0xFF) << 16) |
+                           (((unsigned)((int)roundf(f.w * id)) & 0xFF) << 24);
+        qrow[lay::q8_word(b, l)] = (int)w;
+    }
+    drow[lay::q8_scale(K, b)] = db;
+}
+
+__device__ inline void quant_block(const float (&v)[32], int K, size_t row, int b, int8_t *qs, float *d, float *s)
+{
+    quant_block_at(v, K, b, reinterpret_cast<int *>(qs + row * K), d + row * (K / 32), s + row * (K / 32));
 }
 
 // 32 consecutive floats, 16-byte aligned
@@ -656,7 +688,7 @@ constexpr int XT = 8; // activation rows staged in LDS at a time
 
 // Each wave holds NSET sets of rows (four groups each), all loaded before the
 // first token: more bytes in flight per wave.
-template <int TY, int K, bool GATEUP, bool DUMP, int NSET>
+template <int TY, int K, bool GATEUP, bool DUMP, int NSET, bool QX>
 __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
 {
     constexpr int S = K / 64;
@@ -692,46 +724,61 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
     }
     const int rows = M.rows;
     const int row0 = (blockIdx.x * MV_WAVES + wave) * RPW * NSET + (GATEUP ? grp >> 1 : grp);
-    // The slot's activation rows, XT at a time, staged in LDS by the whole
+    // The slot's activation rows, XC at a time, staged in LDS by the whole
     // workgroup (every group of every wave reads them from there), loaded
-    // straight from global memory into LDS.  Row j of a chunk is ROW16
-    // 16-byte pieces: its K/16 quant pieces, then its K/128 scale pieces.
+    // straight from global memory into LDS.  Staged row j is ROW16 16-byte
+    // pieces: its K/16 quant pieces, then its K/128 scale pieces.  With QX
+    // the rows come in as f32 (a.xf) and the workgroup quantises them itself
+    // (Q8Act, as the standalone quantiser), XC of them in 16 KB.
+    static_assert(!QX || TY != T_Q4K, "Q4_K needs the block sums of a separate quantisation");
+    constexpr int XC = QX ? (XT * 512 / K > 0 ? XT * 512 / K : 1) : XT;
     constexpr int ROW16 = K / 16 + K / 128;
     constexpr int NTH = MV_WAVES * WAVE;
-    constexpr int NPC = (XT * ROW16 + NTH - 1) / NTH; // pieces per thread
-    __shared__ int4 stage[NPC * NTH];
-    // piece idx of the chunk at i0 (nt rows; xr: its row in xq / xd) lands in stage[idx]
-    auto stage_piece = [&](int c, int idx, int xr) {
-        const int r = idx % ROW16;
-        const uint8_t *src = r < K / 16 ? reinterpret_cast<const uint8_t *>(a.xq) + (size_t)xr * K + 16 * r
-                                        : reinterpret_cast<const uint8_t *>(a.xd) + (size_t)xr * (K / 8) + 16 * (r - K / 16);
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)&stage[c * NTH + wave * WAVE], 16,
-                                         0, 0);
+    constexpr int NPC = QX ? XC * K / 4 / NTH : (XC * ROW16 + NTH - 1) / NTH; // pieces per thread
+    __shared__ int4 stage[(XC * ROW16 + NTH - 1) / NTH * NTH];
+    __shared__ int4 fstage[QX ? NPC * NTH : 1];
+    auto lds_load = [&](const void *src, int4 *dst_wave) {
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst_wave, 16, 0, 0);
+    };
+    // issue the loads of the nt rows of the chunk at i0 (row numbers of the
+    // first chunk from the slot record: scalar loads, which do not wait on
+    // vector loads); pieces past the chunk reread a valid row into unused LDS
+    auto issue_chunk = [&](int i0, int nt) {
+        if constexpr (QX) {
+#pragma unroll
+            for (int c = 0; c < NPC; c++) {
+                const int idx0 = (int)threadIdx.x + c * NTH, idx = idx0 < nt * (K / 4) ? idx0 : nt * (K / 4) - 1;
+                lds_load(a.xf + (size_t)(beg + i0) * K + 4 * idx, &fstage[c * NTH + wave * WAVE]);
+            }
+        } else {
+            int trow[XC];
+#pragma unroll
+            for (int j = 0; j < XC; j++) {
+                const int i = i0 + min(j, nt - 1);
+                trow[j] = !a.x_by_token ? beg + i
+                          : shared      ? tok0 + i
+                          : i0 == 0     ? (j < nt ? sl.tok[j] : sl.tok[0])
+                                        : a.dp.pair_tok[beg + i];
+            }
+#pragma unroll
+            for (int c = 0; c < NPC; c++) {
+                if (c * NTH >= nt * ROW16) break; // uniform
+                const int idx0 = (int)threadIdx.x + c * NTH, idx = idx0 < nt * ROW16 ? idx0 : nt * ROW16 - 1;
+                const int jr = idx / ROW16, r = idx % ROW16;
+                int xr = trow[0];
+#pragma unroll
+                for (int jj = 1; jj < XC; jj++) xr = jr == jj ? trow[jj] : xr;
+                const uint8_t *src = r < K / 16
+                                         ? reinterpret_cast<const uint8_t *>(a.xq) + (size_t)xr * K + 16 * r
+                                         : reinterpret_cast<const uint8_t *>(a.xd) + (size_t)xr * (K / 8) + 16 * (r - K / 16);
+                lds_load(src, &stage[c * NTH + wave * WAVE]);
+            }
+        }
     };
     // The first chunk's loads go out before the weights': loads complete in
     // order, so a gather issued after the weight loads would start only once
-    // the weights are in.  Its row numbers are in the slot record (scalar
-    // loads, which do not wait on vector loads).  Pieces past the chunk
-    // reread a valid row into unused LDS.
-    {
-        const int nt = min(XT, cnt);
-        int trow[XT];
-#pragma unroll
-        for (int j = 0; j < XT; j++) {
-            const int i = min(j, cnt - 1);
-            trow[j] = a.x_by_token ? (shared ? tok0 + i : (j < cnt ? sl.tok[j] : sl.tok[0])) : beg + i;
-        }
-#pragma unroll
-        for (int c = 0; c < NPC; c++) {
-            if (c * NTH >= nt * ROW16) break; // uniform
-            const int idx0 = (int)threadIdx.x + c * NTH, idx = idx0 < nt * ROW16 ? idx0 : nt * ROW16 - 1;
-            const int j = idx / ROW16;
-            int xr = trow[0];
-#pragma unroll
-            for (int jj = 1; jj < XT; jj++) xr = j == jj ? trow[jj] : xr;
-            stage_piece(c, idx, xr);
-        }
-    }
+    // the weights are in.
+    issue_chunk(0, min(XC, cnt));
     Chain<TY, K> wc[NSET];
 #pragma unroll
     for (int q = 0; q < NSET; q++) {
@@ -739,18 +786,21 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
         wc[q].load(M, (size_t)e * rows + (row < rows ? row : 0), pi, l);
     }
     int32_t *dump = DUMP ? (m ? a.dump_b : a.dump_a) : nullptr;
-    for (int i0 = 0; i0 < cnt; i0 += XT) {
-        const int nt = min(XT, cnt - i0);
-        if (i0 > 0) { // the first chunk is on its way
-#pragma unroll
-            for (int c = 0; c < NPC; c++) {
-                if (c * NTH >= nt * ROW16) break;
-                const int idx0 = (int)threadIdx.x + c * NTH, idx = idx0 < nt * ROW16 ? idx0 : nt * ROW16 - 1;
-                const int i = i0 + idx / ROW16;
-                stage_piece(c, idx, a.x_by_token ? (shared ? tok0 + i : a.dp.pair_tok[beg + i]) : beg + i);
-            }
-        }
+    for (int i0 = 0; i0 < cnt; i0 += XC) {
+        const int nt = min(XC, cnt - i0);
+        if (i0 > 0) issue_chunk(i0, nt);
         __syncthreads();
+        if constexpr (QX) {
+            // one thread per 32-element block of the chunk
+            const int b = threadIdx.x;
+            if (b < nt * (K / 32)) {
+                const int jr = b / (K / 32), bb = b % (K / 32);
+                quant_block_lds(reinterpret_cast<const float4 *>(&fstage[0]) + jr * (K / 4) + bb * 8, K, bb,
+                                reinterpret_cast<int *>(&stage[jr * ROW16]),
+                                reinterpret_cast<float *>(&stage[jr * ROW16 + K / 16]));
+            }
+            __syncthreads();
+        }
         for (int j = 0; j < nt; j++) {
             const int i = i0 + j;
             const size_t xrow =
@@ -838,8 +888,23 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a)
     *po = a.add ? *po + o : o;
 }
 
+template <int TY, int KK, bool GATEUP, bool DUMP, bool QX>
+hipError_t launch_case(const MvArgs &a, int rows, int slots, hipStream_t st)
+{
+    if constexpr (QX && TY == T_Q4K) {
+        return hipErrorInvalidValue; // Q4_K takes the separately quantised rows (with block sums)
+    } else {
+        // row sets per wave: the shorter the rows, the more of them in flight
+        constexpr int NSET = KK >= 2048 ? MV_NSET_LONG : MV_NSET_SHORT;
+        const int rows_per_wg = MV_WAVES * (GATEUP ? 2 : 4) * NSET;
+        dim3 grid((rows + rows_per_wg - 1) / rows_per_wg, slots);
+        k_chain_mv<TY, KK, GATEUP, DUMP, NSET, QX><<<grid, MV_WAVES * WAVE, 0, st>>>(a);
+        return hipGetLastError();
+    }
+}
+
 // One launch over the routed slots (routed = 1) and/or the shared expert.
-template <bool GATEUP, bool DUMP>
+template <bool GATEUP, bool DUMP, bool QX>
 hipError_t launch_mv_t(MvArgs a, int routed, int shared, hipStream_t st)
 {
     const DevMat &M = routed ? a.a : a.sa;
@@ -848,16 +913,8 @@ hipError_t launch_mv_t(MvArgs a, int routed, int shared, hipStream_t st)
     a.n_sh = shared ? (a.T + XT - 1) / XT : 0;
     const int slots = a.u_max + a.n_sh;
     if (slots == 0) return hipSuccess;
-    dim3 block(MV_WAVES * WAVE);
-    // row sets per wave: the shorter the rows, the more of them in flight
 #define BIV_MV_CASE(TY, KK)                                                                                     \
-    if (M.ty == TY && M.cols == KK) {                                                                           \
-        constexpr int NSET = KK >= 2048 ? MV_NSET_LONG : MV_NSET_SHORT;                                         \
-        const int rows_per_wg = MV_WAVES * (GATEUP ? 2 : 4) * NSET;                                             \
-        dim3 grid((M.rows + rows_per_wg - 1) / rows_per_wg, slots);                                             \
-        k_chain_mv<TY, KK, GATEUP, DUMP, NSET><<<grid, block, 0, st>>>(a);                                      \
-        return hipGetLastError();                                                                               \
-    }
+    if (M.ty == TY && M.cols == KK) return launch_case<TY, KK, GATEUP, DUMP, QX>(a, M.rows, slots, st);
     BIV_MV_CASE(T_Q8_0, 2048)
     BIV_MV_CASE(T_Q8_0, 1024)
     BIV_MV_CASE(T_Q8_0, 512)
@@ -871,19 +928,28 @@ hipError_t launch_mv_t(MvArgs a, int routed, int shared, hipStream_t st)
     return hipErrorInvalidValue;
 }
 
+template <bool GATEUP, bool QX>
+hipError_t launch_mv_q(const MvArgs &a, int routed, int shared, hipStream_t st)
+{
+    const bool dump = a.dump_a || a.dump_b;
+    return dump ? launch_mv_t<GATEUP, true, QX>(a, routed, shared, st) : launch_mv_t<GATEUP, false, QX>(a, routed, shared, st);
+}
+
 template <bool GATEUP>
 hipError_t launch_mv(const MvArgs &a, hipStream_t st)
 {
-    const bool dump = a.dump_a || a.dump_b;
+    auto go = [&](int routed, int shared) {
+        return !GATEUP && a.xf ? launch_mv_q<GATEUP, !GATEUP>(a, routed, shared, st)
+                               : launch_mv_q<GATEUP, false>(a, routed, shared, st);
+    };
     const bool has_shared = a.sa.q != nullptr;
     // routed and shared in one launch when they share types and shape
     const bool together = has_shared && a.sa.ty == a.a.ty && a.sa.cols == a.a.cols && a.sa.rows == a.a.rows &&
                           (!GATEUP || a.sb.ty == a.b.ty);
-    if (together)
-        return dump ? launch_mv_t<GATEUP, true>(a, 1, 1, st) : launch_mv_t<GATEUP, false>(a, 1, 1, st);
-    hipError_t err = dump ? launch_mv_t<GATEUP, true>(a, 1, 0, st) : launch_mv_t<GATEUP, false>(a, 1, 0, st);
+    if (together) return go(1, 1);
+    hipError_t err = go(1, 0);
     if (err != hipSuccess || !has_shared) return err;
-    return dump ? launch_mv_t<GATEUP, true>(a, 0, 1, st) : launch_mv_t<GATEUP, false>(a, 0, 1, st);
+    return go(0, 1);
 }
 
 } // namespace

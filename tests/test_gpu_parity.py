@@ -118,8 +118,9 @@ def full_parity(orc, engine, layer, moe, h, block_dots=True):
 
 @pytest.mark.parametrize("T", [1, 2, 5, 9, 64, 65, 100])
 def test_q8_small_layer(orc, engine, T):
-    """T <= 64 runs the three-launch decode kernels, T > 64 the six-launch
-    path with token-chunked slots; both must give the oracle's bits."""
+    """T <= 16 quantises the SwiGLU intermediate inside the down kernel,
+    larger T in its own launch; T > 64 cuts an expert's pairs into slots of
+    16.  All must give the oracle's bits."""
     print(f"case q8 small T={T}", flush=True)
     layer, moe = layer_for(engine, seed=21, n_expert=32)
     h = synth.make_tokens(100 + T, T, offsets=True)
