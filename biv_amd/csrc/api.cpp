@@ -380,7 +380,6 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     a.T = T;
     a.P = P;
     a.u_max = u_max;
-    a.x_by_token = 1;
     HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
     MARK();
     const int rows_act = has_shared ? P + T : P;
@@ -407,7 +406,6 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     d.T = T;
     d.P = P;
     d.u_max = u_max;
-    d.x_by_token = 0;
     HIP_TRY(ctx, biv::launch_down(d, st), "expert down");
     MARK();
     HIP_TRY(ctx,

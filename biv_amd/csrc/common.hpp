@@ -98,7 +98,6 @@ struct MvArgs {
     int u_max;              // grid slots of the routed experts (max_slots)
     int n_sh;               // grid slots of the shared expert, which come first (set by the launcher)
     int sh_chunk;           // tokens per shared-expert slot (set by the launcher)
-    int x_by_token;         // 1: input row of a pair is its token's (gate/up); 0: the pair's own (down)
 };
 
 // gate/up: out[p][r] = silu(gate_r . x) * (up_r . x) for every pair and shared row.

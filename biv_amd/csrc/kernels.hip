@@ -159,13 +159,46 @@ __device__ inline bool finishing_workgroup(int *counter, int total)
 // wave runs FMA chain L over elements L, L+32, ... of one row; then the tree
 // (acc0+acc1)+(acc2+acc3) and hsum (quant.rs:1149-1153).  Rows are stored in
 // the f32 chain layout, so each lane's 4-value steps are one 128-bit load.
+//
+// A workgroup holds 8 rows in registers and meets TC tokens, staged in LDS in
+// the same chain layout (each lane's 4-value steps one 128-bit LDS read);
+// tokens go two at a time, two independent chains per lane.
 template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(RouterArgs a)
 {
     constexpr int E = 32 * NS;
     const float *__restrict__ router = a.router;
-    const float *__restrict__ gate_inp = a.gate_inp;
     const float *__restrict__ h = a.h;
     const int n_expert = a.n_expert, T = a.T;
+    const int L = threadIdx.x & 31;
+    const int row = blockIdx.x * (blockDim.x / 32) + (threadIdx.x >> 5);
+    const bool valid = row < n_expert || (row == n_expert && a.gate_inp != nullptr);
+    // gate_inp as an offset from the router: one pointer, a per-lane offset
+    const float *w = router + (row < n_expert ? (ptrdiff_t)row * E : (valid ? a.gate_inp - router : 0));
+    float wv[NS];
+    {
+        const float4 *p = reinterpret_cast<const float4 *>(w);
+#pragma unroll
+        for (int i = 0; i < NS / 4; i++) {
+            float4 v = p[i * 32 + L];
+            wv[4 * i] = v.x;
+            wv[4 * i + 1] = v.y;
+            wv[4 * i + 2] = v.z;
+            wv[4 * i + 3] = v.w;
+        }
+    }
+    // this workgroup's tokens into LDS, in the chain layout
+    __shared__ float4 xs[TC][E / 4];
+    const int t0 = blockIdx.y * TC, nt = min(TC, T - t0);
+    for (int idx = threadIdx.x; idx < nt * (E / 4); idx += blockDim.x) {
+        const int t = idx / (E / 4), e = 4 * (idx % (E / 4));
+        const float4 v = reinterpret_cast<const float4 *>(h + (size_t)(t0 + t) * E)[e / 4];
+        float *dst = reinterpret_cast<float *>(xs[t]);
+        // element e + c is value e >> 5 of chain (e + c) & 31
+        dst[lay::f32_elem(e >> 5, (e & 31))] = v.x;
+        dst[lay::f32_elem(e >> 5, (e & 31) + 1)] = v.y;
+        dst[lay::f32_elem(e >> 5, (e & 31) + 2)] = v.z;
+        dst[lay::f32_elem(e >> 5, (e & 31) + 3)] = v.w;
+    }
     // the Q8 activations of h, for the experts: every thread of the grid
     // takes blocks of 32 in turn
     {
@@ -176,31 +209,8 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
             quant_block(v, E, i / (E / 32), i % (E / 32), a.xq, a.xd, a.xs);
         }
     }
-    const int L = threadIdx.x & 31;
-    const int row = blockIdx.x * (blockDim.x / 32) + (threadIdx.x >> 5);
-    const bool valid = row < n_expert || (row == n_expert && gate_inp != nullptr);
-    const float *w = row < n_expert ? router + (size_t)row * E : gate_inp;
-    float wv[NS];
-    if (valid) {
-        const float4 *p = reinterpret_cast<const float4 *>(w);
-#pragma unroll
-        for (int i = 0; i < NS / 4; i++) {
-            float4 v = p[i * 32 + L];
-            wv[4 * i] = v.x;
-            wv[4 * i + 1] = v.y;
-            wv[4 * i + 2] = v.z;
-            wv[4 * i + 3] = v.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < NS; i++) wv[i] = 0.0f;
-    }
-    const int t_end = min(T, (int)(blockIdx.y + 1) * TC);
-    for (int t = blockIdx.y * TC; t < t_end; t++) {
-        const float *x = h + (size_t)t * E + L;
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NS; i++) acc = fmaf(wv[i], x[32 * i], acc);
+    __syncthreads();
+    auto finish = [&](float acc, int t) {
         float v = acc;
         v = v + __shfl_xor(v, 8);  // acc0+acc1 (lanes 0-7), acc2+acc3 (16-23)
         v = v + __shfl_xor(v, 16); // (acc0+acc1)+(acc2+acc3)
@@ -211,6 +221,36 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
             if (row < n_expert) a.logits[(size_t)t * n_expert + row] = v;
             else a.glogit[t] = v;
         }
+    };
+    int t = 0;
+    for (; t + 1 < nt; t += 2) {
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NS / 4; q++) {
+            const float4 x0 = xs[t][q * 32 + L], x1 = xs[t + 1][q * 32 + L];
+            acc0 = fmaf(wv[4 * q], x0.x, acc0);
+            acc1 = fmaf(wv[4 * q], x1.x, acc1);
+            acc0 = fmaf(wv[4 * q + 1], x0.y, acc0);
+            acc1 = fmaf(wv[4 * q + 1], x1.y, acc1);
+            acc0 = fmaf(wv[4 * q + 2], x0.z, acc0);
+            acc1 = fmaf(wv[4 * q + 2], x1.z, acc1);
+            acc0 = fmaf(wv[4 * q + 3], x0.w, acc0);
+            acc1 = fmaf(wv[4 * q + 3], x1.w, acc1);
+        }
+        finish(acc0, t0 + t);
+        finish(acc1, t0 + t + 1);
+    }
+    if (t < nt) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NS / 4; q++) {
+            const float4 x0 = xs[t][q * 32 + L];
+            acc = fmaf(wv[4 * q], x0.x, acc);
+            acc = fmaf(wv[4 * q + 1], x0.y, acc);
+            acc = fmaf(wv[4 * q + 2], x0.z, acc);
+            acc = fmaf(wv[4 * q + 3], x0.w, acc);
+        }
+        finish(acc, t0 + t);
     }
 }
 
@@ -688,8 +728,9 @@ constexpr int XT = 8; // activation rows staged in LDS at a time
 
 // Each wave holds NSET sets of rows (four groups each), all loaded before the
 // first token: more bytes in flight per wave.
-template <int TY, int K, bool GATEUP, bool DUMP, int NSET, bool QX>
-__global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
+// WPE: the waves per SIMD the register allocation must allow.
+template <int TY, int K, bool GATEUP, bool DUMP, int NSET, bool QX, int WPE>
+__global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(WPE, 8))) void k_chain_mv(MvArgs a)
 {
     constexpr int S = K / 64;
     constexpr int RPW = GATEUP ? 2 : 4; // rows per set of a wave
@@ -751,26 +792,28 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
                 lds_load(a.xf + (size_t)(beg + i0) * K + 4 * idx, &fstage[c * NTH + wave * WAVE]);
             }
         } else {
+            // the input row of staged row j: gate/up reads its pair's token's
+            // row (from the slot record for the first chunk), down the pair's own
             int trow[XC];
 #pragma unroll
             for (int j = 0; j < XC; j++) {
                 const int i = i0 + min(j, nt - 1);
-                trow[j] = !a.x_by_token ? beg + i
-                          : shared      ? tok0 + i
-                          : i0 == 0     ? (j < nt ? sl.tok[j] : sl.tok[0])
-                                        : a.dp.pair_tok[beg + i];
+                trow[j] = !GATEUP   ? beg + i
+                          : shared  ? tok0 + i
+                          : i0 == 0 ? (j < nt ? sl.tok[j] : sl.tok[0])
+                                    : a.dp.pair_tok[beg + i];
             }
 #pragma unroll
             for (int c = 0; c < NPC; c++) {
                 if (c * NTH >= nt * ROW16) break; // uniform
                 const int idx0 = (int)threadIdx.x + c * NTH, idx = idx0 < nt * ROW16 ? idx0 : nt * ROW16 - 1;
-                const int jr = idx / ROW16, r = idx % ROW16;
+                const int jr = idx / ROW16, r = idx - jr * ROW16;
                 int xr = trow[0];
 #pragma unroll
                 for (int jj = 1; jj < XC; jj++) xr = jr == jj ? trow[jj] : xr;
-                const uint8_t *src = r < K / 16
-                                         ? reinterpret_cast<const uint8_t *>(a.xq) + (size_t)xr * K + 16 * r
-                                         : reinterpret_cast<const uint8_t *>(a.xd) + (size_t)xr * (K / 8) + 16 * (r - K / 16);
+                // quant pieces, then scale pieces (16 bytes each)
+                const uint8_t *src = r < K / 16 ? reinterpret_cast<const uint8_t *>(a.xq) + (size_t)xr * K + 16 * r
+                                                : reinterpret_cast<const uint8_t *>(a.xd) + (size_t)xr * (K / 8) + 16 * (r - K / 16);
                 lds_load(src, &stage[c * NTH + wave * WAVE]);
             }
         }
@@ -803,8 +846,7 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) void k_chain_mv(MvArgs a)
         }
         for (int j = 0; j < nt; j++) {
             const int i = i0 + j;
-            const size_t xrow =
-                a.x_by_token ? (size_t)(shared ? tok0 + i : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
+            const size_t xrow = GATEUP ? (size_t)(shared ? tok0 + i : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
             const size_t orow = (size_t)(beg + i);
             int xw[S];
             float xd[S];
@@ -898,7 +940,10 @@ hipError_t launch_case(const MvArgs &a, int rows, int slots, hipStream_t st)
         constexpr int NSET = KK >= 2048 ? MV_NSET_LONG : MV_NSET_SHORT;
         const int rows_per_wg = MV_WAVES * (GATEUP ? 2 : 4) * NSET;
         dim3 grid((rows + rows_per_wg - 1) / rows_per_wg, slots);
-        k_chain_mv<TY, KK, GATEUP, DUMP, NSET, QX><<<grid, MV_WAVES * WAVE, 0, st>>>(a);
+        // occupancy asked of the register allocator (Q8_0 only: the K-quant
+        // chains need more registers than 4 waves per SIMD leave)
+        constexpr int WPE = TY != T_Q8_0 || DUMP ? 1 : KK >= 2048 && !QX ? 5 : 4;
+        k_chain_mv<TY, KK, GATEUP, DUMP, NSET, QX, WPE><<<grid, MV_WAVES * WAVE, 0, st>>>(a);
         return hipGetLastError();
     }
 }
@@ -957,13 +1002,16 @@ hipError_t launch_mv(const MvArgs &a, hipStream_t st)
 hipError_t launch_router(const RouterArgs &a, hipStream_t st)
 {
     const int rows = a.n_expert + 1;
-    // 8 rows per workgroup; tokens split over grid.y in chunks of TC
-    const int tc = a.T <= 16 ? 16 : 32;
-    dim3 grid((rows + 7) / 8, (a.T + tc - 1) / tc);
+    // 8 rows per workgroup; tokens split over grid.y in chunks of TC (32 KB of
+    // LDS, 64 KB past 8 tokens)
 #define BIV_ROUTER_CASE(NS)                                                                                     \
     if (a.E == 32 * NS) {                                                                                       \
-        if (tc == 16) k_router<NS, 16><<<grid, 256, 0, st>>>(a);                                                \
-        else k_router<NS, 32><<<grid, 256, 0, st>>>(a);                                                         \
+        constexpr int TC = 8192 / (32 * NS);                                                                    \
+        if (a.T <= 2 * TC) {                                                                                    \
+            k_router<NS, TC><<<dim3((rows + 7) / 8, (a.T + TC - 1) / TC), 256, 0, st>>>(a);                     \
+        } else {                                                                                                \
+            k_router<NS, 2 * TC><<<dim3((rows + 7) / 8, (a.T + 2 * TC - 1) / (2 * TC)), 256, 0, st>>>(a);      \
+        }                                                                                                       \
         return hipGetLastError();                                                                               \
     }
     BIV_ROUTER_CASE(64)
