@@ -160,8 +160,7 @@ __device__ inline bool finishing_workgroup(int *counter, int total)
 // (acc0+acc1)+(acc2+acc3) and hsum (quant.rs:1149-1153).  Rows are stored in
 // the f32 chain layout, so each lane's 4-value steps are one 128-bit load.
 //
-// A workgroup holds 8 rows in registers and meets TC tokens, staged in LDS in
-// the same chain layout (each lane's 4-value steps one 128-bit LDS read);
+// A workgroup holds 8 rows in registers and meets TC tokens, staged in LDS;
 // tokens go two at a time, two independent chains per lane.
 template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(RouterArgs a)
 {
@@ -186,18 +185,21 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
             wv[4 * i + 3] = v.w;
         }
     }
-    // this workgroup's tokens into LDS, in the chain layout
-    __shared__ float4 xs[TC][E / 4];
+    // this workgroup's tokens into LDS (row-major, straight from global
+    // memory; pieces past the last token reread it into unused LDS)
+    __shared__ float xs[TC][E];
     const int t0 = blockIdx.y * TC, nt = min(TC, T - t0);
-    for (int idx = threadIdx.x; idx < nt * (E / 4); idx += blockDim.x) {
-        const int t = idx / (E / 4), e = 4 * (idx % (E / 4));
-        const float4 v = reinterpret_cast<const float4 *>(h + (size_t)(t0 + t) * E)[e / 4];
-        float *dst = reinterpret_cast<float *>(xs[t]);
-        // element e + c is value e >> 5 of chain (e + c) & 31
-        dst[lay::f32_elem(e >> 5, (e & 31))] = v.x;
-        dst[lay::f32_elem(e >> 5, (e & 31) + 1)] = v.y;
-        dst[lay::f32_elem(e >> 5, (e & 31) + 2)] = v.z;
-        dst[lay::f32_elem(e >> 5, (e & 31) + 3)] = v.w;
+    {
+        constexpr int NP = TC * (E / 4) / 256; // 16-byte pieces per thread
+        const float4 *src = reinterpret_cast<const float4 *>(h + (size_t)t0 * E);
+        float4 *dst = reinterpret_cast<float4 *>(&xs[0][0]) + (threadIdx.x & ~(WAVE - 1));
+#pragma unroll
+        for (int c = 0; c < NP; c++) {
+            if (c * 256 >= nt * (E / 4)) break; // uniform
+            const int idx0 = c * 256 + (int)threadIdx.x, idx = idx0 < nt * (E / 4) ? idx0 : nt * (E / 4) - 1;
+            __builtin_amdgcn_global_load_lds(src + idx, (__attribute__((address_space(3))) void *)(dst + c * 256), 16, 0,
+                                             0);
+        }
     }
     // the Q8 activations of h, for the experts: every thread of the grid
     // takes blocks of 32 in turn
@@ -222,20 +224,14 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
             else a.glogit[t] = v;
         }
     };
+    // chain L meets elements L, L + 32, ... (conflict-free 32-bit reads)
     int t = 0;
     for (; t + 1 < nt; t += 2) {
         float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
-        for (int q = 0; q < NS / 4; q++) {
-            const float4 x0 = xs[t][q * 32 + L], x1 = xs[t + 1][q * 32 + L];
-            acc0 = fmaf(wv[4 * q], x0.x, acc0);
-            acc1 = fmaf(wv[4 * q], x1.x, acc1);
-            acc0 = fmaf(wv[4 * q + 1], x0.y, acc0);
-            acc1 = fmaf(wv[4 * q + 1], x1.y, acc1);
-            acc0 = fmaf(wv[4 * q + 2], x0.z, acc0);
-            acc1 = fmaf(wv[4 * q + 2], x1.z, acc1);
-            acc0 = fmaf(wv[4 * q + 3], x0.w, acc0);
-            acc1 = fmaf(wv[4 * q + 3], x1.w, acc1);
+        for (int i = 0; i < NS; i++) {
+            acc0 = fmaf(wv[i], xs[t][32 * i + L], acc0);
+            acc1 = fmaf(wv[i], xs[t + 1][32 * i + L], acc1);
         }
         finish(acc0, t0 + t);
         finish(acc1, t0 + t + 1);
@@ -243,13 +239,7 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
     if (t < nt) {
         float acc = 0.0f;
 #pragma unroll
-        for (int q = 0; q < NS / 4; q++) {
-            const float4 x0 = xs[t][q * 32 + L];
-            acc = fmaf(wv[4 * q], x0.x, acc);
-            acc = fmaf(wv[4 * q + 1], x0.y, acc);
-            acc = fmaf(wv[4 * q + 2], x0.z, acc);
-            acc = fmaf(wv[4 * q + 3], x0.w, acc);
-        }
+        for (int i = 0; i < NS; i++) acc = fmaf(wv[i], xs[t][32 * i + L], acc);
         finish(acc, t0 + t);
     }
 }
