@@ -168,6 +168,19 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
     const float *__restrict__ router = a.router;
     const float *__restrict__ h = a.h;
     const int n_expert = a.n_expert, T = a.T;
+    // Workgroups past the row groups quantise h for the experts (Q8 rows in
+    // the chain layout): one 32-element block per thread and turn.
+    const int n_rw = (n_expert + 1 + 7) / 8;
+    if ((int)blockIdx.x >= n_rw) {
+        const int nq = gridDim.x - n_rw, nthreads = nq * gridDim.y * blockDim.x;
+        for (int i = ((blockIdx.x - n_rw) * gridDim.y + blockIdx.y) * blockDim.x + threadIdx.x; i < T * (E / 32);
+             i += nthreads) {
+            float v[32];
+            load32(h + 32 * (size_t)i, v);
+            quant_block(v, E, i / (E / 32), i % (E / 32), a.xq, a.xd, a.xs);
+        }
+        return;
+    }
     const int L = threadIdx.x & 31;
     const int row = blockIdx.x * (blockDim.x / 32) + (threadIdx.x >> 5);
     const bool valid = row < n_expert || (row == n_expert && a.gate_inp != nullptr);
@@ -199,16 +212,6 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
             const int idx0 = c * 256 + (int)threadIdx.x, idx = idx0 < nt * (E / 4) ? idx0 : nt * (E / 4) - 1;
             __builtin_amdgcn_global_load_lds(src + idx, (__attribute__((address_space(3))) void *)(dst + c * 256), 16, 0,
                                              0);
-        }
-    }
-    // the Q8 activations of h, for the experts: every thread of the grid
-    // takes blocks of 32 in turn
-    {
-        const int nthreads = gridDim.x * gridDim.y * blockDim.x;
-        for (int i = (blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < T * (E / 32); i += nthreads) {
-            float v[32];
-            load32(h + 32 * (size_t)i, v);
-            quant_block(v, E, i / (E / 32), i % (E / 32), a.xq, a.xd, a.xs);
         }
     }
     __syncthreads();
@@ -992,15 +995,19 @@ hipError_t launch_mv(const MvArgs &a, hipStream_t st)
 hipError_t launch_router(const RouterArgs &a, hipStream_t st)
 {
     const int rows = a.n_expert + 1;
+    // quantisation workgroups beside the row groups: about one block per thread
+    const int qblocks = a.T * (a.E / 32);
     // 8 rows per workgroup; tokens split over grid.y in chunks of TC (32 KB of
     // LDS, 64 KB past 8 tokens)
 #define BIV_ROUTER_CASE(NS)                                                                                     \
     if (a.E == 32 * NS) {                                                                                       \
         constexpr int TC = 8192 / (32 * NS);                                                                    \
         if (a.T <= 2 * TC) {                                                                                    \
-            k_router<NS, TC><<<dim3((rows + 7) / 8, (a.T + TC - 1) / TC), 256, 0, st>>>(a);                     \
+            const int gy = (a.T + TC - 1) / TC;                                                                 \
+            k_router<NS, TC><<<dim3((rows + 7) / 8 + (qblocks + 256 * gy - 1) / (256 * gy), gy), 256, 0, st>>>(a); \
         } else {                                                                                                \
-            k_router<NS, 2 * TC><<<dim3((rows + 7) / 8, (a.T + 2 * TC - 1) / (2 * TC)), 256, 0, st>>>(a);      \
+            const int gy = (a.T + 2 * TC - 1) / (2 * TC);                                                       \
+            k_router<NS, 2 * TC><<<dim3((rows + 7) / 8 + (qblocks + 256 * gy - 1) / (256 * gy), gy), 256, 0, st>>>(a); \
         }                                                                                                       \
         return hipGetLastError();                                                                               \
     }
