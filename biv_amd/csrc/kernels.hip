@@ -488,9 +488,87 @@ __device__ void sort_pairs(const int *__restrict__ ids, const float *__restrict_
     }
 }
 
-// One wavefront per token routes it, then one workgroup sorts: with a single
-// workgroup (T <= RS_WAVES) from LDS, else the workgroup that finishes
-// routing last, from global memory.
+// LDS writes of this wavefront visible to all its lanes
+__device__ inline void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The same dispatch as sort_pairs for P <= 4 * WAVE pairs, by one wavefront
+// and without workgroup barriers.  A pair's place among its expert's pairs is
+// the number of earlier pairs with that expert (a token names an expert at
+// most once, so pair order is token order).  cnt, first and sfirst are LDS
+// arrays of MAX_EXPERTS.
+__device__ void sort_pairs_wave(const int *ids, const float *wts, int n_expert, int k, int T, int chunk,
+                                const Dispatch &dp, int *cnt, int *first, int *sfirst)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int P = T * k;
+    for (int e = lane; e < MAX_EXPERTS; e += WAVE) cnt[e] = 0;
+    wave_lds_sync();
+    for (int i = lane; i < P; i += WAVE) atomicAdd(&cnt[ids[i]], 1);
+    wave_lds_sync();
+    // lane owns experts 4 lane .. 4 lane + 3: their pairs and slots, then a
+    // wave scan of the lane totals
+    constexpr int EPL = MAX_EXPERTS / WAVE;
+    int c[EPL], ns[EPL], tot = 0, stot = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const int e = EPL * lane + j;
+        c[j] = e < n_expert ? cnt[e] : 0;
+        ns[j] = (c[j] + chunk - 1) / chunk;
+        tot += c[j];
+        stot += ns[j];
+    }
+    int x = tot, y = stot;
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+        const int xs = __shfl_up(x, off), ys = __shfl_up(y, off);
+        if (lane >= off) {
+            x += xs;
+            y += ys;
+        }
+    }
+    const int n_used = __shfl(y, WAVE - 1);
+    int pos = x - tot, spos = y - stot;
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const int e = EPL * lane + j;
+        if (e < n_expert) {
+            first[e] = pos;
+            sfirst[e] = spos;
+            for (int q = 0; q < ns[j]; q++)
+                reinterpret_cast<int4 *>(&dp.slots[spos + q])[0] =
+                    make_int4(e, pos + q * chunk, min(chunk, c[j] - q * chunk), 0);
+        }
+        pos += c[j];
+        spos += ns[j];
+    }
+    for (int u = n_used + lane; u < dp.slot_cap; u += WAVE) reinterpret_cast<int4 *>(&dp.slots[u])[0] = make_int4(0, 0, 0, 0);
+    wave_lds_sync();
+    for (int i = lane; i < P; i += WAVE) {
+        const int e = ids[i], t = i / k;
+        int r = 0;
+        for (int j = 0; j < i; j++) r += ids[j] == e;
+        const int p = first[e] + r;
+        dp.pair_tok[p] = t;
+        dp.pair_exp[p] = e;
+        dp.pair_w[p] = wts[i];
+        // positions ascend with the expert id: the pair's place among the
+        // token's k is the number of its experts below e
+        int rank = 0;
+        for (int j2 = 0; j2 < k; j2++) rank += ids[t * k + j2] < e;
+        dp.tok_pairs[(size_t)t * k + rank] = p;
+        if (r % chunk < SLOT_TOKS) dp.slots[sfirst[e] + r / chunk].tok[r % chunk] = t;
+    }
+}
+
+// One wavefront per token routes it, then the pairs are sorted: with a
+// single workgroup (T <= RS_WAVES, so at most 4 * WAVE pairs as k <= 16) by
+// one wavefront from LDS, else by the workgroup that finishes routing last,
+// from global memory.
 constexpr int RS_WAVES = RS_THREADS / WAVE;
 
 __global__ __launch_bounds__(RS_THREADS) void k_route_sort(const float *__restrict__ logits, int n_expert, int k,
@@ -505,8 +583,10 @@ __global__ __launch_bounds__(RS_THREADS) void k_route_sort(const float *__restri
         route_token(logits, n_expert, k, t, es[wave], dp.ids, dp.wts, single ? lds_ids : nullptr,
                     single ? lds_wts : nullptr);
     if (single) {
+        // the routes from LDS, sorted by one wavefront
+        __shared__ int cnt[MAX_EXPERTS], first[MAX_EXPERTS], sfirst[MAX_EXPERTS];
         __syncthreads();
-        sort_pairs<RS_THREADS>(lds_ids, lds_wts, n_expert, k, T, chunk, dp);
+        if (wave == 0) sort_pairs_wave(lds_ids, lds_wts, n_expert, k, T, chunk, dp, cnt, first, sfirst);
         return;
     }
     if (!finishing_workgroup(counter, gridDim.x)) return;
