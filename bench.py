@@ -102,12 +102,15 @@ def bench_gpu(eng, moes, layer, T, steps, warmup, torch):
         "stage_us": {k: round(v, 3) for k, v in stage_us.items()},
         "wall_s": round(wall, 3),
     }
+    # the dominant kernel alone: launched back to back over the layer copies
+    # (the stage events above add a dispatch gap to every stage)
     dom = max(("gate_up", "down", "router"), key=lambda s: stage_us[s])
+    kern_us = 1e3 * eng.time_stage(moes, h_dev.data_ptr(), T, out_dev.data_ptr(), dom, steps)
     dbytes = stage_bytes(dom, U, T)
-    ach = dbytes / (stage_us[dom] * 1e-6) / 1e9
+    ach = dbytes / (kern_us * 1e-6) / 1e9
     res["roofline"] = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK / 1e9,
                        "unit": "GB/s", "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": None,
-                       "bytes_per_launch": dbytes, "avg_us": round(stage_us[dom], 3)}
+                       "bytes_per_launch": dbytes, "avg_us": round(kern_us, 3)}
     return res
 
 

@@ -324,15 +324,18 @@ struct StageMarks {
     }
 };
 
-// Queue the whole block: h and out are device pointers.
+// Queue the whole block: h and out are device pointers.  With only >= 0,
+// queue stage `only` alone (for measurement: the scratch holds a forward's
+// routing of the same T).
 int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float *out, unsigned flags,
-            const Dumps &dm)
+            const Dumps &dm, int only = -1)
 {
     if (T == 0) return 0;
     int rc = scratch_fit(ctx, m, T);
     if (rc) return rc;
     StageMarks mk(ctx);
-#define MARK() HIP_TRY(ctx, mk.mark(), "timing event")
+#define MARK() HIP_TRY(ctx, only < 0 ? mk.mark() : hipSuccess, "timing event")
+    auto run = [&](int stage) { return only < 0 || only == stage; };
     Scratch &s = ctx->sc;
     hipStream_t st = ctx->stream;
     const int E = m->E, ff = m->ff, ne = m->n_expert, k = m->k;
@@ -358,9 +361,9 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     ra.xd = s.xd;
     ra.xs = s.xs;
     MARK();
-    HIP_TRY(ctx, biv::launch_router(ra, st), "router");
+    if (run(0)) HIP_TRY(ctx, biv::launch_router(ra, st), "router");
     MARK();
-    HIP_TRY(ctx, biv::launch_route_sort(s.logits, ne, k, T, chunk, s.dp, ctr_rs, st), "route and dispatch");
+    if (run(1)) HIP_TRY(ctx, biv::launch_route_sort(s.logits, ne, k, T, chunk, s.dp, ctr_rs, st), "route and dispatch");
     MARK();
 
     biv::MvArgs a{};
@@ -380,7 +383,7 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     a.T = T;
     a.P = P;
     a.u_max = u_max;
-    HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
+    if (run(2)) HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
     MARK();
     const int rows_act = has_shared ? P + T : P;
     // For small T the down kernel quantises its rows itself, saving a launch
@@ -389,7 +392,7 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     // mins need the block sums.  The taps still want the rows apart.
     const bool fused_quant =
         T <= 16 && m->down->m.ty != biv::T_Q4K && (!has_shared || m->sd->m.ty != biv::T_Q4K);
-    if (!fused_quant || dm.act)
+    if ((!fused_quant || dm.act) && run(3))
         HIP_TRY(ctx, biv::launch_quant_rows(s.act, rows_act * ff / 32, ff, s.aq, s.ad, s.as, st), "quantise act");
     MARK();
 
@@ -406,11 +409,13 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     d.T = T;
     d.P = P;
     d.u_max = u_max;
-    HIP_TRY(ctx, biv::launch_down(d, st), "expert down");
+    if (run(4)) HIP_TRY(ctx, biv::launch_down(d, st), "expert down");
     MARK();
-    HIP_TRY(ctx,
-            biv::launch_combine(s.y, s.dp, s.glogit, has_shared, T, P, k, E, out, (flags & BIV_HIP_ADD) != 0, st),
-            "combine");
+    if (run(5))
+        HIP_TRY(ctx,
+                biv::launch_combine(s.y, s.dp, s.glogit, has_shared, T, P, k, E, out, (flags & BIV_HIP_ADD) != 0,
+                                    st),
+                "combine");
     MARK();
 #undef MARK
     return 0;
@@ -736,6 +741,40 @@ int biv_hip_stage_times(biv_hip_ctx *ctx, double *ms, int n_stages, int *n_forwa
     if (n_forwards) *n_forwards = (int)ctx->ev_fwd.size();
     ctx->ev_fwd.clear();
     return 0;
+}
+
+int biv_hip_time_stage(biv_hip_ctx *ctx, const biv_hip_moe *const *moes, int n_moes, const float *h_dev, int n,
+                       float *out_dev, int stage, int reps, double *ms_per_launch)
+{
+    if (!ctx || !moes || n_moes < 1 || !h_dev || !out_dev || n < 1 || stage < 0 || stage >= N_STAGES || reps < 1 ||
+        !ms_per_launch)
+        return fail(ctx, BIV_HIP_E_INVALID, "time_stage: bad arguments");
+    const biv_hip_moe *m0 = moes[0];
+    for (int i = 0; i < n_moes; i++) {
+        const biv_hip_moe *m = moes[i];
+        if (!m || m->E != m0->E || m->ff != m0->ff || m->n_expert != m0->n_expert || m->k != m0->k ||
+            (m->sg == nullptr) != (m0->sg == nullptr) || m->gate->m.ty != m0->gate->m.ty ||
+            m->down->m.ty != m0->down->m.ty)
+            return fail(ctx, BIV_HIP_E_INVALID, "time_stage: layers differ in shape or types");
+    }
+    HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    const bool timing = ctx->timing;
+    ctx->timing = false;
+    int rc = forward(ctx, m0, h_dev, n, out_dev, 0, Dumps{}); // the routing the stage runs on
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!rc && hipEventCreate(&e0) != hipSuccess) rc = fail(ctx, BIV_HIP_E_DEVICE, "event");
+    if (!rc && hipEventCreate(&e1) != hipSuccess) rc = fail(ctx, BIV_HIP_E_DEVICE, "event");
+    if (!rc && hipEventRecord(e0, ctx->stream) != hipSuccess) rc = fail(ctx, BIV_HIP_E_DEVICE, "event");
+    for (int r = 0; r < reps && !rc; r++) rc = forward(ctx, moes[r % n_moes], h_dev, n, out_dev, 0, Dumps{}, stage);
+    float ms = 0.0f;
+    if (!rc && hipEventRecord(e1, ctx->stream) != hipSuccess) rc = fail(ctx, BIV_HIP_E_DEVICE, "event");
+    if (!rc && hipEventSynchronize(e1) != hipSuccess) rc = fail(ctx, BIV_HIP_E_DEVICE, "event sync");
+    if (!rc && hipEventElapsedTime(&ms, e0, e1) != hipSuccess) rc = fail(ctx, BIV_HIP_E_DEVICE, "event time");
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    ctx->timing = timing;
+    if (!rc) *ms_per_launch = ms / reps;
+    return rc;
 }
 
 } // extern "C"

@@ -29,7 +29,7 @@ SYMBOLS = [
     "biv_hip_upload_weight", "biv_hip_upload_experts", "biv_hip_moe_create", "biv_hip_moe_forward",
     "biv_hip_moe_forward_device", "biv_hip_moe_forward_taps", "biv_hip_malloc", "biv_hip_free",
     "biv_hip_memcpy_h2d", "biv_hip_memcpy_d2h", "biv_hip_numerics", "biv_hip_device_bytes",
-    "biv_hip_set_timing", "biv_hip_stage_times",
+    "biv_hip_set_timing", "biv_hip_stage_times", "biv_hip_time_stage",
 ]
 
 STAGES = ["router", "route_sort", "gate_up", "quant_act", "down", "combine"]
@@ -82,6 +82,8 @@ def load():
     L.biv_hip_device_bytes.restype = sz
     L.biv_hip_set_timing.argtypes = [vp, i]
     L.biv_hip_stage_times.argtypes = [vp, ctypes.POINTER(ctypes.c_double), i, ctypes.POINTER(ctypes.c_int)]
+    L.biv_hip_time_stage.argtypes = [vp, ctypes.POINTER(ctypes.c_void_p), i, vp, i, vp, i, i,
+                                     ctypes.POINTER(ctypes.c_double)]
     _lib = L
     return L
 
@@ -237,3 +239,13 @@ class HipEngine:
         n = ctypes.c_int()
         self._check(self.L.biv_hip_stage_times(self.h, ms, len(STAGES), ctypes.byref(n)))
         return dict(zip(STAGES, list(ms))), n.value
+
+    def time_stage(self, moes, h_dev, n, out_dev, stage, reps):
+        """ms per launch of one stage (a name of STAGES) run alone, back to
+        back, over the layers `moes` in turn (after one full forward of the
+        first for the routing)."""
+        arr = (ctypes.c_void_p * len(moes))(*[m.handle for m in moes])
+        ms = ctypes.c_double()
+        self._check(self.L.biv_hip_time_stage(self.h, arr, len(moes), h_dev, n, out_dev, STAGES.index(stage), reps,
+                                              ctypes.byref(ms)))
+        return ms.value

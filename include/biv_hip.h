@@ -163,6 +163,18 @@ size_t biv_hip_device_bytes(const biv_hip_ctx *ctx);
 int biv_hip_set_timing(biv_hip_ctx *ctx, int enable);
 int biv_hip_stage_times(biv_hip_ctx *ctx, double *ms, int n_stages, int *n_forwards);
 
+/* Measurement of one stage alone (index as in biv_hip_stage_times): runs one
+ * forward of moes[0] on the n tokens at h_dev (for its routing and
+ * dispatch), then launches that stage reps times back to back on the
+ * context's stream, layer moes[r % n_moes] at launch r (layers of the same
+ * shape and types, e.g. copies in HBM so that weights are not re-read from
+ * cache), between two events; writes the milliseconds per launch.  A stage a
+ * forward skips (the separate quantisation when the down kernel quantises)
+ * measures the empty stream.  No counterpart in the reference, which times
+ * whole passes only (src/bench.rs:86-103). */
+int biv_hip_time_stage(biv_hip_ctx *ctx, const biv_hip_moe *const *moes, int n_moes, const float *h_dev, int n,
+                       float *out_dev, int stage, int reps, double *ms_per_launch);
+
 #ifdef __cplusplus
 }
 #endif

@@ -154,6 +154,29 @@ def test_q8_prefill_zipf_512(orc, engine, skew):
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
 
 
+@pytest.mark.parametrize("groups", [8, 12, 5])
+def test_router_ties(orc, engine, groups):
+    """Router rows repeated (row i = row i % groups), so logits tie exactly:
+    ties inside the top k must come out lowest expert first, and ties across
+    the k-th place take the slow selection over every probability."""
+    import dataclasses
+    print(f"case router ties groups={groups}", flush=True)
+    layer = synth.make_layer(seed=71, n_expert=32)
+    W = layer.router.data.view(np.float32).reshape(32, -1).copy()
+    W[:] = W[np.arange(32) % groups]
+    layer = dataclasses.replace(layer, router=dataclasses.replace(layer.router, data=W.view(np.uint8).reshape(-1)))
+    moe = engine.moe(layer)
+    for T in (1, 3, 8, 12):
+        h = synth.make_tokens(400 + T, T, offsets=True)
+        rel, t = full_parity(orc, engine, layer, moe, h, block_dots=False)
+        ids = t["ids"]
+        for tok in range(T):  # tied experts in ascending order
+            ww = t["weights"][tok]
+            for r in range(layer.k - 1):
+                if ww[r] == ww[r + 1]:
+                    assert ids[tok, r] < ids[tok, r + 1]
+
+
 def test_kquant_layer(orc, engine):
     """Q4_K gate/up, Q6_K down (config 4) at small expert count."""
     print("case kquant", flush=True)
