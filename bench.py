@@ -49,8 +49,8 @@ def stage_bytes(stage, U, T):
         return (U + 1) * 2 * FF * Q8_ROW_E + T * E * 9 // 8 + R * FF * 4
     if stage == "quant_act":
         return R * FF * 4 + R * FF * 9 // 8
-    if stage == "down":  # weights, Q8 intermediate, y
-        return (U + 1) * E * Q8_ROW_FF + R * FF * 9 // 8 + R * E * 4
+    if stage == "down":  # weights, the intermediate (f32 when the kernel quantises it, T <= 16), y
+        return (U + 1) * E * Q8_ROW_FF + R * FF * (4 if T <= 16 else 9 / 8) + R * E * 4
     if stage == "combine":
         return R * E * 4 + T * E * 4 + P * 8
     if stage == "router":  # router + gate_inp, h, logits, Q8 h
@@ -58,6 +58,15 @@ def stage_bytes(stage, U, T):
     if stage == "route_sort":
         return T * NE * 4 + P * 24
     return 0
+
+
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
+# (scaled by a copy kernel of known size: x2.0 and x1.0) on this workload:
+# profiles/moe_layer_q8_0_hbm_traffic.md.  Keyed by (stage, T).
+TRAFFIC = {
+    ("gate_up", 1): 20207131, ("gate_up", 5): 91705677, ("gate_up", 40): 430113924,
+    ("down", 1): 10344203, ("down", 5): 46907741, ("down", 40): 217679560,
+}
 
 
 def tokens_for(layer, T, seed):
@@ -109,7 +118,7 @@ def bench_gpu(eng, moes, layer, T, steps, warmup, torch):
     dbytes = stage_bytes(dom, U, T)
     ach = dbytes / (kern_us * 1e-6) / 1e9
     res["roofline"] = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK / 1e9,
-                       "unit": "GB/s", "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": None,
+                       "unit": "GB/s", "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": TRAFFIC.get((dom, T)),
                        "bytes_per_launch": dbytes, "avg_us": round(kern_us, 3)}
     return res
 
@@ -143,6 +152,9 @@ def main():
     ap.add_argument("--T", type=int, default=5, help="tokens per step of the headline workload")
     ap.add_argument("--sweep", default="1,40,512", help="other T values to report ('' for none)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 to skip)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="first copy this many MiB device to device (a kernel of known traffic, to scale "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counts)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -151,6 +163,11 @@ def main():
 
     import torch
     from biv_amd import hip, synth
+    if args.copy_mib:
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device="cuda")
+        torch.empty_like(src).copy_(src)
+        torch.cuda.synchronize()
+        del src
     t = time.perf_counter()
     layer = synth.make_layer(1)
     log(f"layer generated in {time.perf_counter() - t:.1f}s")
