@@ -109,7 +109,10 @@ bool block_of(int ty, size_t &be, size_t &bb)
 }
 
 // Types the expert kernels compute with.
-bool expert_type_ok(int ty) { return ty == BIV_GGML_Q8_0 || ty == BIV_GGML_Q4_K || ty == BIV_GGML_Q6_K; }
+bool expert_type_ok(int ty)
+{
+    return ty == BIV_GGML_Q8_0 || ty == BIV_GGML_Q4_K || ty == BIV_GGML_Q6_K || ty == BIV_GGML_BF16;
+}
 
 int dev_alloc(biv_hip_ctx *ctx, size_t bytes, uint8_t **out)
 {
@@ -151,8 +154,8 @@ int upload_mat(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, con
         return fail(ctx, BIV_HIP_E_INVALID, "width %zu: Q8_0/Q4_K rows must be a multiple of 256", cols);
     if (ty == BIV_GGML_Q6_K && cols % 512)
         return fail(ctx, BIV_HIP_E_INVALID, "width %zu: Q6_K rows must be a multiple of 512", cols);
-    if (ty == BIV_GGML_F32 && cols % 128)
-        return fail(ctx, BIV_HIP_E_INVALID, "width %zu: F32 rows must be a multiple of 128", cols);
+    if ((ty == BIV_GGML_F32 || ty == BIV_GGML_BF16) && cols % 128)
+        return fail(ctx, BIV_HIP_E_INVALID, "width %zu: F32/BF16 rows must be a multiple of 128", cols);
     const int K = (int)cols;
     std::vector<uint8_t> q(nr * qrow), s(nr * srow), d(nr * drow);
     for (size_t e = 0; e < n; e++)
@@ -202,6 +205,9 @@ int upload_mat(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, con
             case BIV_GGML_F32:
                 for (int e2 = 0; e2 < K; e2++)
                     memcpy(qd + 4 * biv::lay::f32_elem(e2 / 32, e2 % 32), src + 4 * e2, 4);
+                break;
+            case BIV_GGML_BF16:
+                for (int e2 = 0; e2 < K; e2++) memcpy(qd + 2 * biv::lay::bf16_elem(e2), src + 2 * e2, 2);
                 break;
             default:
                 memcpy(qd, src, row_bytes);
@@ -376,6 +382,7 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     a.xq = s.xq;
     a.xd = s.xd;
     a.xs = s.xs;
+    a.xf = h; // BF16 matrices take the f32 rows (Input::F32, ops.rs:45-60)
     a.dp = s.dp;
     a.out = s.act;
     a.dump_a = dm.gate;
@@ -390,9 +397,13 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     // (every workgroup of a slot quantises the slot's rows: past a few tokens
     // that costs more than it saves), unless a down matrix is Q4_K, whose
     // mins need the block sums.  The taps still want the rows apart.
-    const bool fused_quant =
-        T <= 16 && m->down->m.ty != biv::T_Q4K && (!has_shared || m->sd->m.ty != biv::T_Q4K);
-    if ((!fused_quant || dm.act) && run(3))
+    // BF16 down matrices take the f32 intermediate as it is (no Q8, as
+    // uses_f32_act, quant.rs:75-77).
+    const bool down_f32 = m->down->m.ty == biv::T_BF16 && (!has_shared || m->sd->m.ty == biv::T_BF16);
+    const bool down_q8 = m->down->m.ty != biv::T_BF16 || (has_shared && m->sd->m.ty != biv::T_BF16);
+    const bool fused_quant = T <= 16 && !down_f32 && m->down->m.ty != biv::T_Q4K &&
+                             (!has_shared || (m->sd->m.ty != biv::T_Q4K && m->sd->m.ty != biv::T_BF16));
+    if (down_q8 && (!fused_quant || dm.act) && run(3))
         HIP_TRY(ctx, biv::launch_quant_rows(s.act, rows_act * ff / 32, ff, s.aq, s.ad, s.as, st), "quantise act");
     MARK();
 
@@ -402,7 +413,8 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     d.xq = s.aq;
     d.xd = s.ad;
     d.xs = s.as;
-    d.xf = fused_quant ? s.act : nullptr;
+    d.xf = s.act;
+    d.qx = fused_quant;
     d.dp = s.dp;
     d.out = s.y;
     d.dump_a = dm.down;
@@ -537,8 +549,8 @@ int biv_hip_moe_create(biv_hip_ctx *ctx, const biv_hip_weight *router, const biv
     const int E = g.cols, ff = g.rows, ne = g.n;
     if (r.ty != BIV_GGML_F32) return fail(ctx, BIV_HIP_E_TYPE, "router type %d: only F32 routers", r.ty);
     if (!expert_type_ok(g.ty) || !expert_type_ok(u.ty) || !expert_type_ok(d.ty))
-        return fail(ctx, BIV_HIP_E_TYPE, "expert types %d/%d/%d: kernels exist for Q8_0, Q4_K, Q6_K", g.ty, u.ty,
-                    d.ty);
+        return fail(ctx, BIV_HIP_E_TYPE, "expert types %d/%d/%d: kernels exist for Q8_0, Q4_K, Q6_K, BF16", g.ty,
+                    u.ty, d.ty);
     if (g.ty != u.ty) return fail(ctx, BIV_HIP_E_TYPE, "gate and up experts must share a type");
     if (u.cols != E || u.rows != ff || u.n != ne || d.cols != ff || d.rows != E || d.n != ne)
         return fail(ctx, BIV_HIP_E_INVALID, "expert shapes disagree: gate %dx%dx%d up %dx%dx%d down %dx%dx%d", g.cols,

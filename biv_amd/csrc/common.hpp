@@ -88,8 +88,9 @@ struct MvArgs {
     const int8_t *xq;       // input rows: int8 [rows_in][K], chain layout
     const float *xd;        // [rows_in][K/32] block scales
     const float *xs;        // [rows_in][K/32] block d * sum(q) (Q4_K mins)
-    const float *xf;        // down only, optional: f32 input rows [rows_in][K], quantised in the kernel
-                            // (then xq / xd / xs are not read; not with Q4_K matrices)
+    const float *xf;        // the f32 input rows [rows_in][K]: what BF16 matrices read, and what the down
+                            // kernel quantises itself when qx is set
+    int qx;                 // down, quantised matrices: quantise xf in the kernel (not with Q4_K)
     Dispatch dp;
     float *out;             // [P + T][rows]
     int32_t *dump_a;        // optional [P + T][rows][K/32] block int32 dots of a
@@ -102,7 +103,7 @@ struct MvArgs {
 
 // gate/up: out[p][r] = silu(gate_r . x) * (up_r . x) for every pair and shared row.
 hipError_t launch_gateup(const MvArgs &a, hipStream_t st);
-// down: out[p][r] = down_r . x_p, with x_p = Q8Act(xf[p]) when a.xf is set
+// down: out[p][r] = down_r . x_p, with x_p = Q8Act(xf[p]) when a.qx is set
 hipError_t launch_down(const MvArgs &a, hipStream_t st);
 // Q8Act of n_blocks 32-element blocks of rows of K, into the chain layout
 hipError_t launch_quant_rows(const float *x, int n_blocks, int K, int8_t *qs, float *d, float *s, hipStream_t st);

@@ -714,6 +714,30 @@ template <int K> struct Chain<T_Q6K, K> {
     __device__ inline float wscale(int s) const { return dd[s >> 2]; }
 };
 
+// BF16: dot_bf16 (quant.rs:1228-1256) with f32 activations; chain L = 8 pi + l
+// holds elements L, L + 16, ... (layout.hpp bf16_elem), two per register.
+template <int K> struct Chain<T_BF16, K> {
+    static constexpr int S = K / 16;
+    int w[S / 2];
+    __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l)
+    {
+        const int4 *q = reinterpret_cast<const int4 *>(M.q + mrow * K * 2);
+#pragma unroll
+        for (int g = 0; g < S / 8; g++) {
+            const int4 v = q[g * 16 + pi * 8 + l];
+            w[4 * g] = v.x;
+            w[4 * g + 1] = v.y;
+            w[4 * g + 2] = v.z;
+            w[4 * g + 3] = v.w;
+        }
+    }
+    __device__ inline float wval(int s) const
+    {
+        const unsigned u = (unsigned)w[s >> 1];
+        return __uint_as_float(s & 1 ? (u & 0xFFFF0000u) : (u << 16));
+    }
+};
+
 // What lane (pi, l) needs of one Q8 activation row: word l of the blocks of
 // parity pi and their scales.
 template <int K> struct XChain {
@@ -844,13 +868,15 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
     // pieces: its K/16 quant pieces, then its K/128 scale pieces.  With QX
     // the rows come in as f32 (a.xf) and the workgroup quantises them itself
     // (Q8Act, as the standalone quantiser), XC of them in 16 KB.
-    static_assert(!QX || TY != T_Q4K, "Q4_K needs the block sums of a separate quantisation");
-    constexpr int XC = QX ? (XT * 512 / K > 0 ? XT * 512 / K : 1) : XT;
+    // BF16 matrices meet the f32 rows themselves (a.xf), XC of them in 16 KB.
+    static_assert(!QX || (TY != T_Q4K && TY != T_BF16), "Q4_K needs the block sums of a separate quantisation");
+    constexpr bool BF = TY == T_BF16, F32IN = QX || BF;
+    constexpr int XC = F32IN ? (XT * 512 / K > 0 ? XT * 512 / K : 1) : XT;
     constexpr int ROW16 = K / 16 + K / 128;
     constexpr int NTH = MV_WAVES * WAVE;
-    constexpr int NPC = QX ? XC * K / 4 / NTH : (XC * ROW16 + NTH - 1) / NTH; // pieces per thread
-    __shared__ int4 stage[(XC * ROW16 + NTH - 1) / NTH * NTH];
-    __shared__ int4 fstage[QX ? NPC * NTH : 1];
+    constexpr int NPC = F32IN ? XC * K / 4 / NTH : (XC * ROW16 + NTH - 1) / NTH; // pieces per thread
+    __shared__ int4 stage[BF ? 1 : (XC * ROW16 + NTH - 1) / NTH * NTH];
+    __shared__ int4 fstage[F32IN ? NPC * NTH : 1];
     auto lds_load = [&](const void *src, int4 *dst_wave) {
         __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst_wave, 16, 0, 0);
     };
@@ -858,24 +884,29 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
     // first chunk from the slot record: scalar loads, which do not wait on
     // vector loads); pieces past the chunk reread a valid row into unused LDS
     auto issue_chunk = [&](int i0, int nt) {
-        if constexpr (QX) {
+        // the input row of staged row j: gate/up reads its pair's token's
+        // row (from the slot record for the first chunk), down the pair's own
+        int trow[XC];
+#pragma unroll
+        for (int j = 0; j < XC; j++) {
+            const int i = i0 + min(j, nt - 1);
+            trow[j] = !GATEUP   ? beg + i
+                      : shared  ? tok0 + i
+                      : i0 == 0 ? (j < nt ? sl.tok[j] : sl.tok[0])
+                                : a.dp.pair_tok[beg + i];
+        }
+        if constexpr (F32IN) {
 #pragma unroll
             for (int c = 0; c < NPC; c++) {
+                if (c * NTH >= nt * (K / 4)) break; // uniform
                 const int idx0 = (int)threadIdx.x + c * NTH, idx = idx0 < nt * (K / 4) ? idx0 : nt * (K / 4) - 1;
-                lds_load(a.xf + (size_t)(beg + i0) * K + 4 * idx, &fstage[c * NTH + wave * WAVE]);
+                const int jr = idx / (K / 4);
+                int xr = trow[0];
+#pragma unroll
+                for (int jj = 1; jj < XC; jj++) xr = jr == jj ? trow[jj] : xr;
+                lds_load(a.xf + (size_t)xr * K + 4 * (idx - jr * (K / 4)), &fstage[c * NTH + wave * WAVE]);
             }
         } else {
-            // the input row of staged row j: gate/up reads its pair's token's
-            // row (from the slot record for the first chunk), down the pair's own
-            int trow[XC];
-#pragma unroll
-            for (int j = 0; j < XC; j++) {
-                const int i = i0 + min(j, nt - 1);
-                trow[j] = !GATEUP   ? beg + i
-                          : shared  ? tok0 + i
-                          : i0 == 0 ? (j < nt ? sl.tok[j] : sl.tok[0])
-                                    : a.dp.pair_tok[beg + i];
-            }
 #pragma unroll
             for (int c = 0; c < NPC; c++) {
                 if (c * NTH >= nt * ROW16) break; // uniform
@@ -917,6 +948,31 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
             }
             __syncthreads();
         }
+        if constexpr (BF) {
+            // BF16: f32 FMA chains over the staged f32 rows
+            for (int j = 0; j < nt; j++) {
+                const size_t orow = (size_t)(beg + i0 + j);
+                const float *xr = reinterpret_cast<const float *>(&fstage[0]) + j * K;
+#pragma unroll
+                for (int q = 0; q < NSET; q++) {
+                    const int row = row0 + q * RPW;
+                    const bool row_ok = row < rows;
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int s = 0; s < K / 16; s++) acc = fmaf(wc[q].wval(s), xr[16 * s + ln], acc);
+                    float t = acc + __shfl_xor(acc, 8); // acc0 + acc1, lane by lane
+                    t = t + __shfl_xor(t, 4);           // the two 128-bit halves
+                    t = t + __shfl_xor(t, 2);           // movehl
+                    t = t + __shfl_xor(t, 1);           // movehdup
+                    if (GATEUP) {
+                        const float up = __shfl_xor(t, 16);
+                        if (m == 0 && ln == 0 && row_ok) a.out[orow * rows + row] = silu_mul(t, up);
+                    } else {
+                        if (ln == 0 && row_ok) a.out[orow * rows + row] = t;
+                    }
+                }
+            }
+        } else {
         for (int j = 0; j < nt; j++) {
             const int i = i0 + j;
             const size_t xrow = GATEUP ? (size_t)(shared ? tok0 + i : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
@@ -971,6 +1027,7 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
                 }
             }
         }
+        }
         __syncthreads();
     }
 }
@@ -1006,8 +1063,10 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a)
 template <int TY, int KK, bool GATEUP, bool DUMP, bool QX>
 hipError_t launch_case(const MvArgs &a, int rows, int slots, hipStream_t st)
 {
-    if constexpr (QX && TY == T_Q4K) {
-        return hipErrorInvalidValue; // Q4_K takes the separately quantised rows (with block sums)
+    if constexpr (QX && (TY == T_Q4K || TY == T_BF16)) {
+        return hipErrorInvalidValue; // Q4_K takes the separately quantised rows (with block sums), BF16 the f32 rows
+    } else if constexpr (DUMP && TY == T_BF16) {
+        return launch_case<TY, KK, GATEUP, false, QX>(a, rows, slots, st); // no integer dots to tap
     } else {
         // row sets per wave: the shorter the rows, the more of them in flight
         constexpr int NSET = KK >= 2048 ? MV_NSET_LONG : MV_NSET_SHORT;
@@ -1042,6 +1101,9 @@ hipError_t launch_mv_t(MvArgs a, int routed, int shared, hipStream_t st)
     BIV_MV_CASE(T_Q6K, 2048)
     BIV_MV_CASE(T_Q6K, 1024)
     BIV_MV_CASE(T_Q6K, 512)
+    BIV_MV_CASE(T_BF16, 2048)
+    BIV_MV_CASE(T_BF16, 1024)
+    BIV_MV_CASE(T_BF16, 512)
 #undef BIV_MV_CASE
     return hipErrorInvalidValue;
 }
@@ -1057,7 +1119,7 @@ template <bool GATEUP>
 hipError_t launch_mv(const MvArgs &a, hipStream_t st)
 {
     auto go = [&](int routed, int shared) {
-        return !GATEUP && a.xf ? launch_mv_q<GATEUP, !GATEUP>(a, routed, shared, st)
+        return !GATEUP && a.qx ? launch_mv_q<GATEUP, !GATEUP>(a, routed, shared, st)
                                : launch_mv_q<GATEUP, false>(a, routed, shared, st);
     };
     const bool has_shared = a.sa.q != nullptr;

@@ -46,5 +46,14 @@ __host__ __device__ constexpr int q6k_sc(int K, int pi, int hsel, int s) { retur
 // chains, chain L summing elements L, L + 32, ...; value i of chain L.
 __host__ __device__ constexpr int f32_elem(int i, int L) { return (((i >> 2) * 32 + L) << 2) + (i & 3); }
 
+// BF16 rows (biv's dot_bf16, quant.rs:1228-1256: two 8-lane accumulators
+// over 16-element steps): chain L (0..15) sums elements L, L + 16, ...;
+// lane L's 128-bit load g holds its steps 8g..8g+7.  Index (in 16-bit
+// units) of element e of a row.
+__host__ __device__ constexpr int bf16_elem(int e)
+{
+    return (((e >> 4) >> 3) * 16 + (e & 15)) * 8 + ((e >> 4) & 7);
+}
+
 } // namespace lay
 } // namespace biv

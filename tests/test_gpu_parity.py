@@ -17,7 +17,7 @@ from biv_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-Q8_0, Q4K, Q6K = synth.Q8_0, synth.Q4K, synth.Q6K
+Q8_0, Q4K, Q6K, BF16 = synth.Q8_0, synth.Q4K, synth.Q6K, synth.BF16
 TOL = 1e-3  # max|d| <= TOL * RMS(reference output)
 
 
@@ -175,6 +175,26 @@ def test_router_ties(orc, engine, groups):
             for r in range(layer.k - 1):
                 if ww[r] == ww[r + 1]:
                     assert ids[tok, r] < ids[tok, r + 1]
+
+
+@pytest.mark.parametrize("T", [1, 5, 17, 64, 100])
+def test_bf16_layer(orc, engine, T):
+    """BF16 experts (config 4): f32 activations, dot_bf16's 16 FMA chains, the
+    f32 intermediate straight into down; no integer dots to tap."""
+    print(f"case bf16 T={T}", flush=True)
+    layer, moe = layer_for(engine, seed=81, n_expert=32, types=(BF16, BF16, BF16))
+    h = synth.make_tokens(500 + T, T, offsets=True)
+    full_parity(orc, engine, layer, moe, h, block_dots=False)
+
+
+@pytest.mark.parametrize("types", [(BF16, BF16, Q8_0), (Q8_0, Q8_0, BF16)])
+def test_bf16_mixed(orc, engine, types):
+    """BF16 beside Q8_0: the intermediate is quantised only for a Q8_0 down."""
+    print(f"case bf16 mixed {types}", flush=True)
+    layer, moe = layer_for(engine, seed=91, n_expert=16, types=types)
+    for T in (3, 20):
+        h = synth.make_tokens(600 + T, T, offsets=True)
+        full_parity(orc, engine, layer, moe, h, block_dots=False)
 
 
 def test_kquant_layer(orc, engine):
