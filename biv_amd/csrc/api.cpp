@@ -755,6 +755,16 @@ int biv_hip_stage_times(biv_hip_ctx *ctx, double *ms, int n_stages, int *n_forwa
     return 0;
 }
 
+int biv_hip_rms_norm(biv_hip_ctx *ctx, float *x_dev, const float *w_dev, int rows, int n, float eps)
+{
+    if (!ctx) return BIV_HIP_E_INVALID;
+    if (rows < 0 || n <= 0 || n % 32 || (rows > 0 && (!x_dev || !w_dev)))
+        return fail(ctx, BIV_HIP_E_INVALID, "rms_norm: %d rows of %d (n a positive multiple of 32)", rows, n);
+    HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    HIP_TRY(ctx, biv::launch_rms_norm(x_dev, w_dev, rows, n, eps, ctx->stream), "rms_norm");
+    return 0;
+}
+
 int biv_hip_time_stage(biv_hip_ctx *ctx, const biv_hip_moe *const *moes, int n_moes, const float *h_dev, int n,
                        float *out_dev, int stage, int reps, double *ms_per_launch)
 {

@@ -248,6 +248,30 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
 }
 
 // ---------------------------------------------------------------------------
+// ops::rms_norm (ops.rs:136-144) of each row of n: ss = dot_f32(g, g) / n in
+// the 32-chain order above, scale = 1 / sqrt(ss + eps), v *= scale * w.  A
+// 32-lane half wave per row; n a multiple of 32.
+__global__ __launch_bounds__(256) void k_rms_norm(float *__restrict__ x, const float *__restrict__ w, int rows, int n,
+                                                  float eps)
+{
+    const int L = threadIdx.x & 31;
+    const int row = blockIdx.x * (blockDim.x / 32) + (threadIdx.x >> 5);
+    if (row >= rows) return; // uniform over the half wave; no shuffles cross halves
+    float *g = x + (size_t)row * n;
+    float acc = 0.0f;
+    for (int i = L; i < n; i += 32) acc = fmaf(g[i], g[i], acc);
+    float v = acc;
+    v = v + __shfl_xor(v, 8);  // acc0+acc1 (lanes 0-7), acc2+acc3 (16-23)
+    v = v + __shfl_xor(v, 16); // (acc0+acc1)+(acc2+acc3)
+    v = v + __shfl_xor(v, 4);  // the two 128-bit halves
+    v = v + __shfl_xor(v, 2);  // movehl
+    v = v + __shfl_xor(v, 1);  // movehdup
+    const float ss = v / (float)n;
+    const float scale = 1.0f / sqrtf(ss + eps);
+    for (int i = L; i < n; i += 32) g[i] = g[i] * (scale * w[i]);
+}
+
+// ---------------------------------------------------------------------------
 // route (model.rs:256-268): softmax over the token's logits (ops.rs:192-201),
 // the k highest probabilities with the lower expert first among equals, and
 // weights p / max(sum of the k in rank order, 1/16384).  One wavefront per
@@ -1133,6 +1157,13 @@ hipError_t launch_mv(const MvArgs &a, hipStream_t st)
 }
 
 } // namespace
+
+hipError_t launch_rms_norm(float *x, const float *w, int rows, int n, float eps, hipStream_t st)
+{
+    if (rows <= 0) return hipSuccess;
+    k_rms_norm<<<(rows + 7) / 8, 256, 0, st>>>(x, w, rows, n, eps);
+    return hipGetLastError();
+}
 
 hipError_t launch_router(const RouterArgs &a, hipStream_t st)
 {

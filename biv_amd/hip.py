@@ -29,7 +29,7 @@ SYMBOLS = [
     "biv_hip_upload_weight", "biv_hip_upload_experts", "biv_hip_moe_create", "biv_hip_moe_forward",
     "biv_hip_moe_forward_device", "biv_hip_moe_forward_taps", "biv_hip_malloc", "biv_hip_free",
     "biv_hip_memcpy_h2d", "biv_hip_memcpy_d2h", "biv_hip_numerics", "biv_hip_device_bytes",
-    "biv_hip_set_timing", "biv_hip_stage_times", "biv_hip_time_stage",
+    "biv_hip_set_timing", "biv_hip_stage_times", "biv_hip_time_stage", "biv_hip_rms_norm",
 ]
 
 STAGES = ["router", "route_sort", "gate_up", "quant_act", "down", "combine"]
@@ -82,6 +82,7 @@ def load():
     L.biv_hip_device_bytes.restype = sz
     L.biv_hip_set_timing.argtypes = [vp, i]
     L.biv_hip_stage_times.argtypes = [vp, ctypes.POINTER(ctypes.c_double), i, ctypes.POINTER(ctypes.c_int)]
+    L.biv_hip_rms_norm.argtypes = [vp, vp, vp, i, i, ctypes.c_float]
     L.biv_hip_time_stage.argtypes = [vp, ctypes.POINTER(ctypes.c_void_p), i, vp, i, vp, i, i,
                                      ctypes.POINTER(ctypes.c_double)]
     _lib = L
@@ -239,6 +240,27 @@ class HipEngine:
         n = ctypes.c_int()
         self._check(self.L.biv_hip_stage_times(self.h, ms, len(STAGES), ctypes.byref(n)))
         return dict(zip(STAGES, list(ms))), n.value
+
+    def rms_norm_device(self, x_dev, w_dev, rows, n, eps):
+        """ops::rms_norm in place on device memory (queued on the stream)."""
+        self._check(self.L.biv_hip_rms_norm(self.h, x_dev, w_dev, rows, n, eps))
+
+    def rms_norm(self, x, w, eps):
+        """ops::rms_norm of the host rows x [rows, n] by w [n]: a new array."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        rows, n = x.shape
+        xd, wd = self.malloc(x.nbytes), self.malloc(w.nbytes)
+        try:
+            self.h2d(xd, x)
+            self.h2d(wd, w)
+            self.rms_norm_device(xd, wd, rows, n, eps)
+            out = np.empty_like(x)
+            self.d2h(out, xd)
+        finally:
+            self.free(xd)
+            self.free(wd)
+        return out
 
     def time_stage(self, moes, h_dev, n, out_dev, stage, reps):
         """ms per launch of one stage (a name of STAGES) run alone, back to

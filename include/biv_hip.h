@@ -163,6 +163,13 @@ size_t biv_hip_device_bytes(const biv_hip_ctx *ctx);
 int biv_hip_set_timing(biv_hip_ctx *ctx, int enable);
 int biv_hip_stage_times(biv_hip_ctx *ctx, double *ms, int n_stages, int *n_forwards);
 
+/* ops::rms_norm (engine/src/ops.rs:136-144) of `rows` rows of n floats in
+ * device memory, in place: per row ss = dot_f32(g, g) / n (the x86 32-chain
+ * order), scale = 1 / sqrt(ss + eps), v *= scale * w[i].  The norm between
+ * stacked MoE layers (post_norm before Model::ffn, model.rs:786-790).  n is
+ * a multiple of 32.  Queued on the context's stream. */
+int biv_hip_rms_norm(biv_hip_ctx *ctx, float *x_dev, const float *w_dev, int rows, int n, float eps);
+
 /* Measurement of one stage alone (index as in biv_hip_stage_times): runs one
  * forward of moes[0] on the n tokens at h_dev (for its routing and
  * dispatch), then launches that stage reps times back to back on the

@@ -197,6 +197,21 @@ def test_bf16_mixed(orc, engine, types):
         full_parity(orc, engine, layer, moe, h, block_dots=False)
 
 
+@pytest.mark.parametrize("n", [2048, 512, 96])
+def test_rms_norm(orc, engine, n):
+    """ops::rms_norm between stacked layers: the same bits as the oracle's
+    (dot_f32's 32-chain order, IEEE division and square root)."""
+    print(f"case rms_norm n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((37, n)) * rng.uniform(0.01, 100.0, (37, 1))).astype(np.float32)
+    x[3] = 0.0  # an all-zero row: scale 1/sqrt(eps)
+    w = (1.0 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+    for eps in (1e-6, 1e-5):
+        got = engine.rms_norm(x, w, eps)
+        ref = orc.rms_norm(x, w, eps)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), eps
+
+
 def test_kquant_layer(orc, engine):
     """Q4_K gate/up, Q6_K down (config 4) at small expert count."""
     print("case kquant", flush=True)
