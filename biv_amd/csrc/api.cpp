@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 using biv::DevMat;
@@ -158,7 +159,9 @@ int upload_mat(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, con
         return fail(ctx, BIV_HIP_E_INVALID, "width %zu: F32/BF16 rows must be a multiple of 128", cols);
     const int K = (int)cols;
     std::vector<uint8_t> q(nr * qrow), s(nr * srow), d(nr * drow);
-    for (size_t e = 0; e < n; e++)
+    // the matrices of a stack repack on several host threads (disjoint rows)
+    auto repack = [&](size_t e0, size_t e1) {
+    for (size_t e = e0; e < e1; e++)
         for (size_t r = 0; r < rows; r++) {
             const uint8_t *src = src_row(e, r);
             const size_t i = e * rows + r;
@@ -206,14 +209,30 @@ int upload_mat(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, con
                 for (int e2 = 0; e2 < K; e2++)
                     memcpy(qd + 4 * biv::lay::f32_elem(e2 / 32, e2 % 32), src + 4 * e2, 4);
                 break;
-            case BIV_GGML_BF16:
-                for (int e2 = 0; e2 < K; e2++) memcpy(qd + 2 * biv::lay::bf16_elem(e2), src + 2 * e2, 2);
+            case BIV_GGML_BF16: {
+                // element 128 g + 16 m + L goes to (16 g + L) * 8 + m (lay::bf16_elem)
+                uint16_t *dst16 = reinterpret_cast<uint16_t *>(qd);
+                for (int g = 0; g < K / 128; g++)
+                    for (int m = 0; m < 8; m++) {
+                        uint16_t v[16];
+                        memcpy(v, src + 2 * (128 * g + 16 * m), 32);
+                        for (int L = 0; L < 16; L++) dst16[(16 * g + L) * 8 + m] = v[L];
+                    }
                 break;
+            }
             default:
                 memcpy(qd, src, row_bytes);
                 break;
             }
         }
+    };
+    {
+        const size_t nt = std::min<size_t>(n, std::max(1u, std::min(16u, std::thread::hardware_concurrency())));
+        std::vector<std::thread> pool;
+        for (size_t t = 1; t < nt; t++) pool.emplace_back(repack, n * t / nt, n * (t + 1) / nt);
+        repack(0, n / nt);
+        for (auto &th : pool) th.join();
+    }
     int rc;
     if ((rc = dev_alloc(ctx, q.size(), &m.q))) return rc;
     HIP_TRY(ctx, hipMemcpy(m.q, q.data(), q.size(), hipMemcpyHostToDevice), "upload");
@@ -761,8 +780,22 @@ int biv_hip_rms_norm(biv_hip_ctx *ctx, float *x_dev, const float *w_dev, int row
     if (rows < 0 || n <= 0 || n % 32 || (rows > 0 && (!x_dev || !w_dev)))
         return fail(ctx, BIV_HIP_E_INVALID, "rms_norm: %d rows of %d (n a positive multiple of 32)", rows, n);
     HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
-    HIP_TRY(ctx, biv::launch_rms_norm(x_dev, w_dev, rows, n, eps, ctx->stream), "rms_norm");
+    HIP_TRY(ctx, biv::launch_rms_norm(x_dev, x_dev, w_dev, rows, n, eps, ctx->stream), "rms_norm");
     return 0;
+}
+
+int biv_hip_moe_ffn_step(biv_hip_ctx *ctx, const biv_hip_moe *moe, float *x_dev, const float *norm_dev, float eps,
+                         int n)
+{
+    int rc = check_fwd(ctx, moe, x_dev, n, x_dev);
+    if (rc) return rc;
+    if (!norm_dev) return fail(ctx, BIV_HIP_E_INVALID, "null norm weights");
+    if (n == 0) return 0;
+    HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    if ((rc = scratch_fit(ctx, moe, n))) return rc;
+    float *h = ctx->sc.h_stage;
+    HIP_TRY(ctx, biv::launch_rms_norm(x_dev, h, norm_dev, n, moe->E, eps, ctx->stream), "rms_norm");
+    return forward(ctx, moe, h, n, x_dev, BIV_HIP_ADD, Dumps{});
 }
 
 int biv_hip_time_stage(biv_hip_ctx *ctx, const biv_hip_moe *const *moes, int n_moes, const float *h_dev, int n,

@@ -112,8 +112,8 @@ hipError_t launch_quant_rows(const float *x, int n_blocks, int K, int8_t *qs, fl
 hipError_t launch_combine(const float *y, const Dispatch &dp, const float *glogit, int has_shared, int T, int P, int k,
                           int E, float *out, int add, hipStream_t st);
 
-// ops::rms_norm of rows x n in place (n a multiple of 32)
-hipError_t launch_rms_norm(float *x, const float *w, int rows, int n, float eps, hipStream_t st);
+// y = ops::rms_norm(x) of rows x n (y may be x; n a multiple of 32)
+hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, int n, float eps, hipStream_t st);
 
 inline size_t n_counters() { return 1; }
 

@@ -251,13 +251,15 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
 // ops::rms_norm (ops.rs:136-144) of each row of n: ss = dot_f32(g, g) / n in
 // the 32-chain order above, scale = 1 / sqrt(ss + eps), v *= scale * w.  A
 // 32-lane half wave per row; n a multiple of 32.
-__global__ __launch_bounds__(256) void k_rms_norm(float *__restrict__ x, const float *__restrict__ w, int rows, int n,
+// y may be x (in place).
+__global__ __launch_bounds__(256) void k_rms_norm(const float *x, float *y, const float *__restrict__ w, int rows, int n,
                                                   float eps)
 {
     const int L = threadIdx.x & 31;
     const int row = blockIdx.x * (blockDim.x / 32) + (threadIdx.x >> 5);
     if (row >= rows) return; // uniform over the half wave; no shuffles cross halves
-    float *g = x + (size_t)row * n;
+    const float *g = x + (size_t)row * n;
+    float *o = y + (size_t)row * n;
     float acc = 0.0f;
     for (int i = L; i < n; i += 32) acc = fmaf(g[i], g[i], acc);
     float v = acc;
@@ -268,7 +270,7 @@ __global__ __launch_bounds__(256) void k_rms_norm(float *__restrict__ x, const f
     v = v + __shfl_xor(v, 1);  // movehdup
     const float ss = v / (float)n;
     const float scale = 1.0f / sqrtf(ss + eps);
-    for (int i = L; i < n; i += 32) g[i] = g[i] * (scale * w[i]);
+    for (int i = L; i < n; i += 32) o[i] = g[i] * (scale * w[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1158,10 +1160,10 @@ hipError_t launch_mv(const MvArgs &a, hipStream_t st)
 
 } // namespace
 
-hipError_t launch_rms_norm(float *x, const float *w, int rows, int n, float eps, hipStream_t st)
+hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, int n, float eps, hipStream_t st)
 {
     if (rows <= 0) return hipSuccess;
-    k_rms_norm<<<(rows + 7) / 8, 256, 0, st>>>(x, w, rows, n, eps);
+    k_rms_norm<<<(rows + 7) / 8, 256, 0, st>>>(x, y, w, rows, n, eps);
     return hipGetLastError();
 }
 

@@ -30,6 +30,7 @@ SYMBOLS = [
     "biv_hip_moe_forward_device", "biv_hip_moe_forward_taps", "biv_hip_malloc", "biv_hip_free",
     "biv_hip_memcpy_h2d", "biv_hip_memcpy_d2h", "biv_hip_numerics", "biv_hip_device_bytes",
     "biv_hip_set_timing", "biv_hip_stage_times", "biv_hip_time_stage", "biv_hip_rms_norm",
+    "biv_hip_moe_ffn_step",
 ]
 
 STAGES = ["router", "route_sort", "gate_up", "quant_act", "down", "combine"]
@@ -83,6 +84,7 @@ def load():
     L.biv_hip_set_timing.argtypes = [vp, i]
     L.biv_hip_stage_times.argtypes = [vp, ctypes.POINTER(ctypes.c_double), i, ctypes.POINTER(ctypes.c_int)]
     L.biv_hip_rms_norm.argtypes = [vp, vp, vp, i, i, ctypes.c_float]
+    L.biv_hip_moe_ffn_step.argtypes = [vp, vp, vp, vp, ctypes.c_float, i]
     L.biv_hip_time_stage.argtypes = [vp, ctypes.POINTER(ctypes.c_void_p), i, vp, i, vp, i, i,
                                      ctypes.POINTER(ctypes.c_double)]
     _lib = L
@@ -139,6 +141,11 @@ class HipMoe:
         self.ctx._check(self.ctx.L.biv_hip_moe_forward_taps(self.ctx.h, self.handle, _ptr(h), n, _ptr(out),
                                                             ADD if add else 0, ctypes.byref(taps)))
         return out, t
+
+    def ffn_step_device(self, x_dev, norm_dev, eps, n):
+        """The feed-forward half of Model::layer (model.rs:788-790) in device
+        memory: x += moe(rms_norm(x, norm, eps)) for n rows."""
+        self.ctx._check(self.ctx.L.biv_hip_moe_ffn_step(self.ctx.h, self.handle, x_dev, norm_dev, eps, n))
 
     def forward_device(self, h_dev, n, out_dev, add=False):
         """encode_moe's counterpart: device pointers, queued on the context's stream."""

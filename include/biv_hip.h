@@ -170,6 +170,15 @@ int biv_hip_stage_times(biv_hip_ctx *ctx, double *ms, int n_stages, int *n_forwa
  * a multiple of 32.  Queued on the context's stream. */
 int biv_hip_rms_norm(biv_hip_ctx *ctx, float *x_dev, const float *w_dev, int rows, int n, float eps);
 
+/* The feed-forward half of Model::layer for a MoE layer
+ * (engine/src/model.rs:788-790), in device memory: h = rms_norm(x, norm, eps)
+ * (ops::rms_norm_into), then x += moe(h) (ops::add_inplace), for the n rows of
+ * x (n x n_embd floats).  norm_dev holds the layer's post_norm (n_embd
+ * floats).  h lives in the context's scratch.  Queued on the context's
+ * stream. */
+int biv_hip_moe_ffn_step(biv_hip_ctx *ctx, const biv_hip_moe *moe, float *x_dev, const float *norm_dev, float eps,
+                         int n);
+
 /* Measurement of one stage alone (index as in biv_hip_stage_times): runs one
  * forward of moes[0] on the n tokens at h_dev (for its routing and
  * dispatch), then launches that stage reps times back to back on the

@@ -212,6 +212,32 @@ def test_rms_norm(orc, engine, n):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), eps
 
 
+def test_bf16_stack_steps(orc, engine):
+    """Config 4 in small: BF16 layers stacked with the FFN half of
+    Model::layer between them (x += moe(rms_norm(x))), three layers, T=16:
+    the oracle's bits after every layer."""
+    print("case bf16 stack", flush=True)
+    T, E, eps = 16, 2048, 1e-6
+    layers = [synth.make_layer(seed=100 + l, n_expert=32, types=(BF16, BF16, BF16)) for l in range(3)]
+    moes = [engine.moe(l) for l in layers]
+    rng = np.random.default_rng(7)
+    norms = [(1.0 + 0.02 * rng.standard_normal(E)).astype(np.float32) for _ in layers]
+    x = synth.make_tokens(700, T, offsets=True)
+    xd, nd = engine.malloc(x.nbytes), engine.malloc(E * 4)
+    try:
+        engine.h2d(xd, x)
+        ref = x.copy()
+        for layer, moe, w in zip(layers, moes, norms):
+            engine.h2d(nd, w)
+            moe.ffn_step_device(xd, nd, eps, T)
+            got = engine.d2h(np.empty_like(x), xd)
+            ref = ref + orc.moe(layer, orc.rms_norm(ref, w, eps), threads=8)
+            check_output(ref, got)
+    finally:
+        engine.free(xd)
+        engine.free(nd)
+
+
 def test_kquant_layer(orc, engine):
     """Q4_K gate/up, Q6_K down (config 4) at small expert count."""
     print("case kquant", flush=True)
