@@ -123,6 +123,74 @@ def bench_gpu(eng, moes, layer, T, steps, warmup, torch):
     return res
 
 
+def bench_config(eng, layer, copies, T, steps, warmup, torch):
+    """Another layer type (configs[3]: Q4_K gate/up + Q6_K down): the same
+    measurement over `copies` copies in HBM."""
+    moes = [eng.moe(layer) for _ in range(copies)]
+    from biv_amd import synth
+    h = synth.make_tokens(1000 + T, T, offsets=T > 1)  # ~N(0,1) (configs[3])
+    h_dev = torch.from_numpy(h).cuda()
+    out_dev = torch.empty_like(h_dev)
+    for i in range(warmup):
+        moes[i % copies].forward_device(h_dev.data_ptr(), T, out_dev.data_ptr())
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        moes[i % copies].forward_device(h_dev.data_ptr(), T, out_dev.data_ptr())
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    return {"T": T, "us_per_layer": round(ms * 1e3, 3), "tokens_per_s": round(T / (ms * 1e-3), 1),
+            "layers_rotated": copies}
+
+
+def bench_bf16_stack(eng, T, n_layers, passes, torch):
+    """n_layers BF16 MoE layers resident in HBM, a T-token chunk
+    through all of them with the feed-forward half of Model::layer between
+    (x += moe(rms_norm(x)), model.rs:788-790).  The layers are copies of one
+    generated layer (distinct allocations, so every layer's weights come from
+    HBM)."""
+    import numpy as np
+    from biv_amd import synth
+    t = time.perf_counter()
+    layer = synth.make_layer(2, types=(synth.BF16,) * 3)
+    moes = [eng.moe(layer) for _ in range(n_layers)]
+    log(f"bf16 stack: {n_layers} layers uploaded ({eng.device_bytes() / 1e9:.1f} GB on the device) "
+        f"in {time.perf_counter() - t:.1f}s")
+    rng = np.random.default_rng(3)
+    norms = torch.from_numpy((1.0 + 0.02 * rng.standard_normal((n_layers, E))).astype(np.float32)).cuda()
+    x0 = torch.from_numpy(synth.make_tokens(4000, T)).cuda()
+    x = x0.clone()
+    eps = 1e-6
+
+    def one_pass():
+        for l in range(n_layers):
+            moes[l].ffn_step_device(x.data_ptr(), norms[l].data_ptr(), eps, T)
+
+    one_pass()  # warm-up (scratch sized for T)
+    torch.cuda.synchronize()
+    x.copy_(x0)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(passes):
+        one_pass()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / (passes * n_layers)
+    P = T * K
+    flops = 2.0 * (P + T) * 3 * E * FF  # routed pairs and shared rows, gate + up + down
+    U = NE  # every expert is routed at this T
+    layer_bytes = (U + 1) * 3 * E * FF * 2 + ROUTER_BYTES + 2 * T * E * 4
+    return {"T": T, "layers": n_layers, "passes": passes, "us_per_layer": round(ms * 1e3, 1),
+            "tokens_per_s_per_layer": round(T / (ms * 1e-3), 1),
+            "tokens_per_s_stack": round(T / (ms * 1e-3 * n_layers), 1),
+            "compute": "f32 FMA chains (dot_bf16 order)",
+            "roofline": {"bound": "fp32-valu", "achieved": round(flops / (ms * 1e-3) / 1e12, 2),
+                         "peak": 157.3, "unit": "TFLOP/s", "frac": round(flops / (ms * 1e-3) / 157.3e12, 4)},
+            "hbm_GBps": round(layer_bytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def bench_cpu(layer, T, seconds):
     """The oracle (C restatement of biv's AVX2/AVX-VNNI CPU path) on the host cores."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -152,6 +220,10 @@ def main():
     ap.add_argument("--T", type=int, default=5, help="tokens per step of the headline workload")
     ap.add_argument("--sweep", default="1,40,512", help="other T values to report ('' for none)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 to skip)")
+    ap.add_argument("--configs", default="kquant,bf16",
+                    help="other BASELINE configs to run: kquant (Q4_K/Q6_K at T=1, 2048), bf16 (the 40-layer BF16 "
+                         "stack at T=4096); '' for none")
+    ap.add_argument("--bf16-layers", type=int, default=40)
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (a kernel of known traffic, to scale "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counts)")
@@ -188,6 +260,17 @@ def main():
         sweep[str(T)] = bench_gpu(eng, moes, layer, T, steps, args.warmup, torch)
         log(f"T={T}: {sweep[str(T)]}")
 
+    extra = {}
+    todo = {c.strip() for c in args.configs.split(",") if c.strip()}
+    if "kquant" in todo:
+        kq = synth.make_layer(4, types=(synth.Q4K, synth.Q4K, synth.Q6K))
+        extra["kquant_q4k_q6k"] = {str(T): bench_config(eng, kq, 4, T, 50 if T <= 64 else 10, 5, torch)
+                                   for T in (1, 2048)}
+        log(f"kquant: {extra['kquant_q4k_q6k']}")
+    if "bf16" in todo:
+        extra["bf16_stack"] = bench_bf16_stack(eng, 4096, args.bf16_layers, 2, torch)
+        log(f"bf16 stack: {extra['bf16_stack']}")
+
     cpu = None
     if args.cpu_seconds > 0:
         cpu = bench_cpu(layer, args.T, args.cpu_seconds)
@@ -217,6 +300,7 @@ def main():
         "stage_us": main_res["stage_us"],
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "configs": extra,
     }
     print(json.dumps(line), flush=True)
     eng.close()
