@@ -43,6 +43,7 @@ struct Scratch {
     float *ad = nullptr, *as = nullptr;
     float *y = nullptr;
     float *h_stage = nullptr, *o_stage = nullptr;
+    uint8_t *xh = nullptr, *xl = nullptr; // bf16 halves of the matrix-core inputs
     int *counters = nullptr;
     biv::Dispatch dp{};
 };
@@ -292,6 +293,9 @@ int scratch_fit(biv_hip_ctx *ctx, const biv_hip_moe *m, int T)
     rc = rc ? rc : sc_alloc(ctx, R * ff / 32, &s.as);
     rc = rc ? rc : sc_alloc(ctx, R * E, &s.y);
     rc = rc ? rc : sc_alloc(ctx, cap * E, &s.h_stage);
+    // bf16 halves of h or of the intermediate, whichever is larger
+    rc = rc ? rc : sc_alloc(ctx, 2 * std::max((size_t)cap * E, R * ff), &s.xh);
+    rc = rc ? rc : sc_alloc(ctx, 2 * std::max((size_t)cap * E, R * ff), &s.xl);
     rc = rc ? rc : sc_alloc(ctx, cap * E, &s.o_stage);
     rc = rc ? rc : sc_alloc(ctx, ne + P, &s.dp.slots); // >= max_slots(ne, P, chunk)
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_tok);
@@ -318,6 +322,9 @@ struct Dumps {
     int32_t *gate = nullptr, *up = nullptr, *down = nullptr;
     bool act = false; // the quantised intermediate is read back
 };
+
+// T from which BF16 layers use the matrix cores
+constexpr int MFMA_MIN_T = 64;
 
 constexpr int N_STAGES = 6; // router (+ quantise h), route + dispatch, gate/up, quantise act, down, combine
 
@@ -367,9 +374,14 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     const int P = T * k;
     const bool has_shared = m->sg != nullptr;
     int *ctr_rs = s.counters;
+    // BF16 matrices at prefill sizes run on the matrix cores (mfma.hip), when
+    // the routed and shared matrices of that half are all BF16
+    const bool mf_gu = T >= MFMA_MIN_T && m->gate->m.ty == biv::T_BF16 && (!has_shared || m->sg->m.ty == biv::T_BF16);
+    const bool mf_dn = T >= MFMA_MIN_T && m->down->m.ty == biv::T_BF16 && (!has_shared || m->sd->m.ty == biv::T_BF16);
     // pairs per slot: decode keeps an expert's tokens together; larger passes
     // cut them so that hot experts and the shared expert spread over the GPU
-    const int chunk = T <= 64 ? 64 : 16;
+    // (the matrix-core tiles take 128)
+    const int chunk = mf_gu || mf_dn ? 128 : T <= 64 ? 64 : 16;
     const int u_max = biv::max_slots(ne, P, chunk);
     s.dp.slot_cap = u_max;
 
@@ -409,7 +421,28 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     a.T = T;
     a.P = P;
     a.u_max = u_max;
-    if (run(2)) HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
+    if (run(2)) {
+        if (mf_gu) {
+            biv::MfArgs g{};
+            g.a = a.a;
+            g.b = a.b;
+            g.sa = a.sa;
+            g.sb = a.sb;
+            g.xh = reinterpret_cast<const uint4 *>(s.xh);
+            g.xl = reinterpret_cast<const uint4 *>(s.xl);
+            g.dp = s.dp;
+            g.out = s.act;
+            g.T = T;
+            g.P = P;
+            g.u_max = u_max;
+            g.chunk = chunk;
+            g.sh_chunk = 128;
+            HIP_TRY(ctx, biv::launch_split_bf16(h, T, E, s.xh, s.xl, st), "split h");
+            HIP_TRY(ctx, biv::launch_mfma_gateup(g, st), "expert gate/up (mfma)");
+        } else {
+            HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
+        }
+    }
     MARK();
     const int rows_act = has_shared ? P + T : P;
     // For small T the down kernel quantises its rows itself, saving a launch
@@ -440,7 +473,26 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     d.T = T;
     d.P = P;
     d.u_max = u_max;
-    if (run(4)) HIP_TRY(ctx, biv::launch_down(d, st), "expert down");
+    if (run(4)) {
+        if (mf_dn) {
+            biv::MfArgs g{};
+            g.a = d.a;
+            g.sa = d.sa;
+            g.xh = reinterpret_cast<const uint4 *>(s.xh);
+            g.xl = reinterpret_cast<const uint4 *>(s.xl);
+            g.dp = s.dp;
+            g.out = s.y;
+            g.T = T;
+            g.P = P;
+            g.u_max = u_max;
+            g.chunk = chunk;
+            g.sh_chunk = 128;
+            HIP_TRY(ctx, biv::launch_split_bf16(s.act, has_shared ? P + T : P, ff, s.xh, s.xl, st), "split act");
+            HIP_TRY(ctx, biv::launch_mfma_down(g, st), "expert down (mfma)");
+        } else {
+            HIP_TRY(ctx, biv::launch_down(d, st), "expert down");
+        }
+    }
     MARK();
     if (run(5))
         HIP_TRY(ctx,

@@ -112,6 +112,27 @@ hipError_t launch_quant_rows(const float *x, int n_blocks, int K, int8_t *qs, fl
 hipError_t launch_combine(const float *y, const Dispatch &dp, const float *glogit, int has_shared, int T, int P, int k,
                           int E, float *out, int add, hipStream_t st);
 
+// BF16 experts at prefill sizes on the matrix cores (mfma.hip).  The input
+// rows are first split into bf16 hi / lo halves (launch_split_bf16); gate/up
+// writes the f32 SwiGLU intermediate, down the f32 y rows, as the chain
+// kernels do.
+struct MfArgs {
+    DevMat a, b;       // routed stacks, BF16 (b: up)
+    DevMat sa, sb;     // the shared expert's, BF16, sa.q == nullptr without one
+    const uint4 *xh;   // input rows, hi halves: [rows_in][K / 8] 16-byte chunks
+    const uint4 *xl;   // lo halves
+    Dispatch dp;
+    float *out;        // [P + T][rows]
+    int T, P;
+    int u_max;         // grid slots of the routed experts
+    int chunk;         // pairs per routed slot, at most
+    int sh_chunk;      // tokens per shared-expert slot
+    int n_sh;          // set by the launcher
+};
+hipError_t launch_split_bf16(const float *x, int rows, int K, void *xh, void *xl, hipStream_t st);
+hipError_t launch_mfma_gateup(const MfArgs &a, hipStream_t st);
+hipError_t launch_mfma_down(const MfArgs &a, hipStream_t st);
+
 // y = ops::rms_norm(x) of rows x n (y may be x; n a multiple of 32)
 hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, int n, float eps, hipStream_t st);
 
