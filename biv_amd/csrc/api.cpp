@@ -380,8 +380,8 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     const bool mf_dn = T >= MFMA_MIN_T && m->down->m.ty == biv::T_BF16 && (!has_shared || m->sd->m.ty == biv::T_BF16);
     // pairs per slot: decode keeps an expert's tokens together; larger passes
     // cut them so that hot experts and the shared expert spread over the GPU
-    // (the matrix-core tiles take 128)
-    const int chunk = mf_gu || mf_dn ? 128 : T <= 64 ? 64 : 16;
+    // (a matrix-core workgroup takes a whole slot)
+    const int chunk = mf_gu || mf_dn ? biv::MFMA_TOK_TILE : T <= 64 ? 64 : 16;
     const int u_max = biv::max_slots(ne, P, chunk);
     s.dp.slot_cap = u_max;
 
@@ -436,7 +436,7 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
             g.P = P;
             g.u_max = u_max;
             g.chunk = chunk;
-            g.sh_chunk = 128;
+            g.sh_chunk = biv::MFMA_TOK_TILE;
             HIP_TRY(ctx, biv::launch_split_bf16(h, T, E, s.xh, s.xl, st), "split h");
             HIP_TRY(ctx, biv::launch_mfma_gateup(g, st), "expert gate/up (mfma)");
         } else {
@@ -486,7 +486,7 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
             g.P = P;
             g.u_max = u_max;
             g.chunk = chunk;
-            g.sh_chunk = 128;
+            g.sh_chunk = biv::MFMA_TOK_TILE;
             HIP_TRY(ctx, biv::launch_split_bf16(s.act, has_shared ? P + T : P, ff, s.xh, s.xl, st), "split act");
             HIP_TRY(ctx, biv::launch_mfma_down(g, st), "expert down (mfma)");
         } else {

@@ -116,6 +116,9 @@ hipError_t launch_combine(const float *y, const Dispatch &dp, const float *glogi
 // rows are first split into bf16 hi / lo halves (launch_split_bf16); gate/up
 // writes the f32 SwiGLU intermediate, down the f32 y rows, as the chain
 // kernels do.
+// pairs a matrix-core workgroup takes: the slot size for those launches
+constexpr int MFMA_TOK_TILE = 256;
+
 struct MfArgs {
     DevMat a, b;       // routed stacks, BF16 (b: up)
     DevMat sa, sb;     // the shared expert's, BF16, sa.q == nullptr without one
@@ -124,6 +127,7 @@ struct MfArgs {
     Dispatch dp;
     float *out;        // [P + T][rows]
     int T, P;
+    int n_rt;          // row tiles (set by the launcher)
     int u_max;         // grid slots of the routed experts
     int chunk;         // pairs per routed slot, at most
     int sh_chunk;      // tokens per shared-expert slot

@@ -67,24 +67,33 @@ __device__ inline float silu_mul_t(float g, float u, const uint64_t *tab)
 }
 
 // Grouped GEMM over the slots of the dispatch (the shared expert's first):
-// a workgroup takes TOK_TILE pairs of a slot and ROW_TILE output rows; wave
-// (wt, wr) of the 2 x 2 grid takes 64 pairs x 64 rows, as 2 x 2 blocks of
-// 32 x 32.  gate/up: each block has a gate and an up accumulator and the
-// SwiGLU is formed in the epilogue.
+// a workgroup takes a whole slot (up to TOK_TILE pairs) and ROW_TILE output
+// rows; wave (wt, wr) of the 4 x 2 grid takes 64 pairs x 64 rows of each of
+// gate and up (gate/up) or 64 pairs x 128 rows (down), as 32 x 32 blocks, and
+// skips the blocks of pairs past the slot's count.
+// gate/up: each block has a gate and an up accumulator and the SwiGLU is
+// formed in the epilogue.
+//
+// The row tiles of a slot go to one XCD (workgroup ids b, b + 8, ... are
+// dispatched to one XCD): the slot's activation rows come from HBM once per
+// slot and from that XCD's L2 after, and every expert's weights are read
+// once per slot.
 //
 // K advances in stages of 32 (4 chunks, 64 bytes of a row).  A stage's tiles
 // go straight from global memory into LDS (global_load_lds) into a ring of
 // three buffers: the loads of the next two stages are in flight while the
-// waves run this stage's MFMAs from LDS.  LDS layouts: A [half][pair][4], B [row][4], chunk c of row
-// r in slot 4 r + (c ^ ((r >> 2) & 3)): the 64 lanes of a load write 64
-// consecutive slots, 4 lanes reading one row's 64 contiguous bytes, and the
-// swizzle keeps a fragment read (consecutive rows, one chunk) free of bank
-// conflicts.
-constexpr int TOK_TILE = 128;
-constexpr int NWR = 4;              // waves along the rows: a workgroup is 2 x NWR waves
-constexpr int ROW_TILE = 64 * NWR;  // output rows of a workgroup
-constexpr int NTH = 128 * NWR;      // threads of a workgroup
+// waves run this stage's MFMAs from LDS.  LDS layouts: A [half][pair][4], B
+// [row][4], chunk c of row r in slot 4 r + (c ^ ((r >> 2) & 3)): the 64 lanes
+// of a load write 64 consecutive slots, 4 lanes reading one row's 64
+// contiguous bytes, and the swizzle keeps a fragment read (consecutive rows,
+// one chunk) free of bank conflicts.
+constexpr int NWT = 4;              // waves along the pairs
+constexpr int NWR = 2;              // waves along the rows
+constexpr int TOK_TILE = 64 * NWT;  // pairs of a workgroup
+constexpr int NTH = 64 * NWT * NWR; // threads of a workgroup
 constexpr int SK = 4;               // chunks per stage
+constexpr int N_XCD = 8;
+static_assert(TOK_TILE == MFMA_TOK_TILE, "slot size");
 
 template <int K, bool GATEUP>
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_mfma_bf16(MfArgs a)
@@ -92,14 +101,20 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     constexpr int NC = K / 8;          // chunks per row
     constexpr int NS = NC / SK;        // stages
     constexpr int NB = GATEUP ? 2 : 1; // weight matrices
+    constexpr int RB = 4 / NB;         // 32-row blocks of a wave, per matrix
+    constexpr int ROW_TILE = 32 * RB * NWR; // output rows of a workgroup
     constexpr int BR = ROW_TILE * NB;  // weight rows of a tile
     constexpr int A_SLOTS = 2 * SK * TOK_TILE, B_SLOTS = SK * BR;
     static_assert(A_SLOTS % NTH == 0 && B_SLOTS % NTH == 0, "tile shapes");
     __shared__ uint4 sA0[A_SLOTS], sA1[A_SLOTS], sA2[A_SLOTS], sB0[B_SLOTS], sB1[B_SLOTS], sB2[B_SLOTS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 31, kg = lane >> 5;
-    const int wt = wave & 1, wr = wave >> 1;
-    const int u = blockIdx.y;
+    // the two waves of a SIMD (waves w and w + 4) take pairs 64 apart x 2
+    const int wt = wave >> 1, wr = wave & 1;
+    // workgroup -> (slot, row tile): ids b with one b % 8 are one XCD's
+    const int G = N_XCD * a.n_rt, b = blockIdx.x;
+    const int u = (b / G) * N_XCD + b % N_XCD, rt = (b % G) / N_XCD;
+    if (u >= a.u_max + a.n_sh) return;
     const bool shared = u < a.n_sh;
     int e = 0, beg, cnt, tok0 = 0;
     if (shared) {
@@ -113,13 +128,14 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         beg = sl.beg;
         cnt = sl.cnt;
     }
-    const int i0 = blockIdx.z * TOK_TILE; // this workgroup's pairs of the slot
-    if (i0 >= cnt) return;
     const DevMat &Ma = shared ? a.sa : a.a;
     const int rows = Ma.rows;
-    const int r0 = blockIdx.x * ROW_TILE;
+    const int r0 = rt * ROW_TILE;
+    // this wave's 32-pair blocks that hold pairs of the slot
+    const bool live0 = wt * 64 < cnt, live1 = wt * 64 + 32 < cnt;
     // this thread's load slots: slot tid + NTH q is row (tid + NTH q) / 4,
-    // position tid % 4 (the chunk it loads is swizzled by the row)
+    // position tid % 4 (the chunk it loads is swizzled by the row); pairs
+    // past the count load the slot's last pair (unused)
     constexpr int RQ = NTH / SK; // rows a pass of the threads covers
     const int p = tid % SK;
     const uint4 *srcA[2 * TOK_TILE / RQ];
@@ -127,7 +143,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
     for (int q = 0; q < 2 * TOK_TILE / RQ; q++) { // A rows: (half, pair)
         const int tr = (tid + NTH * q) / SK, hl = tr / TOK_TILE, tt = tr % TOK_TILE;
-        const int ti = min(i0 + tt, cnt - 1);
+        const int ti = min(tt, cnt - 1);
         const size_t ar = GATEUP ? (size_t)(shared ? tok0 + ti : a.dp.pair_tok[beg + ti]) : (size_t)(beg + ti);
         srcA[q] = (hl ? a.xl : a.xh) + ar * NC;
         swA[q] = p ^ ((tt >> 2) & 3);
@@ -151,11 +167,11 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         for (int q = 0; q < B_SLOTS / NTH; q++) lds_load(srcB[q] + s * SK + swB[q], sB + NTH * q + 64 * wave);
     };
     auto slot_of = [](int r, int c) { return SK * r + (c ^ ((r >> 2) & 3)); };
-    f32x16 acc[2][2][NB];
+    f32x16 acc[2][RB][NB];
 #pragma unroll
     for (int tb = 0; tb < 2; tb++)
 #pragma unroll
-        for (int rb = 0; rb < 2; rb++)
+        for (int rb = 0; rb < RB; rb++)
 #pragma unroll
             for (int q = 0; q < NB; q++)
 #pragma unroll
@@ -164,23 +180,25 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
         for (int ks = 0; ks < SK / 2; ks++) {
             const int c = 2 * ks + kg;
-            uint4 xa[2][2], wb[2][NB];
+            uint4 xa[2][2], wb[RB][NB];
 #pragma unroll
             for (int tb = 0; tb < 2; tb++)
 #pragma unroll
-                for (int hl = 0; hl < 2; hl++) xa[tb][hl] = sA[slot_of(hl * TOK_TILE + wt * 64 + tb * 32 + li, c)];
+                for (int hl = 0; hl < 2; hl++)
+                    if (tb ? live1 : live0) xa[tb][hl] = sA[slot_of(hl * TOK_TILE + wt * 64 + tb * 32 + li, c)];
 #pragma unroll
-            for (int rb = 0; rb < 2; rb++)
+            for (int rb = 0; rb < RB; rb++)
 #pragma unroll
-                for (int q = 0; q < NB; q++) wb[rb][q] = sB[slot_of(q * ROW_TILE + wr * 64 + rb * 32 + li, c)];
+                for (int q = 0; q < NB; q++) wb[rb][q] = sB[slot_of(q * ROW_TILE + wr * 32 * RB + rb * 32 + li, c)];
             // the halves outermost: consecutive MFMAs feed different
             // accumulators (an MFMA on the accumulator just written waits)
 #pragma unroll
             for (int hl = 0; hl < 2; hl++)
 #pragma unroll
                 for (int tb = 0; tb < 2; tb++)
+                    if (tb ? live1 : live0)
 #pragma unroll
-                    for (int rb = 0; rb < 2; rb++)
+                    for (int rb = 0; rb < RB; rb++)
 #pragma unroll
                         for (int q = 0; q < NB; q++)
                             acc[tb][rb][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
@@ -230,11 +248,11 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
     for (int tb = 0; tb < 2; tb++)
 #pragma unroll
-        for (int rb = 0; rb < 2; rb++)
+        for (int rb = 0; rb < RB; rb++)
 #pragma unroll
             for (int j = 0; j < 16; j++) {
-                const int ti = i0 + wt * 64 + tb * 32 + (j / 4) * 8 + 4 * kg + (j % 4);
-                const int row = r0 + wr * 64 + rb * 32 + li;
+                const int ti = wt * 64 + tb * 32 + (j / 4) * 8 + 4 * kg + (j % 4);
+                const int row = r0 + wr * 32 * RB + rb * 32 + li;
                 if (ti < cnt) {
                     const float v = GATEUP ? silu_mul_t(acc[tb][rb][0][j], acc[tb][rb][NB - 1][j], tab)
                                            : acc[tb][rb][0][j];
@@ -261,9 +279,11 @@ template <bool GATEUP> hipError_t launch_mfma_t(MfArgs a, int routed, int shared
     a.n_sh = shared ? (a.T + a.sh_chunk - 1) / a.sh_chunk : 0;
     const int slots = a.u_max + a.n_sh;
     if (slots == 0) return hipSuccess;
-    if (M.rows % ROW_TILE) return hipErrorInvalidValue;
-    const int maxc = a.chunk > a.sh_chunk ? a.chunk : a.sh_chunk;
-    dim3 grid(M.rows / ROW_TILE, slots, (maxc + TOK_TILE - 1) / TOK_TILE);
+    const int row_tile = 32 * NWR * (GATEUP ? 2 : 4);
+    if (M.rows % row_tile) return hipErrorInvalidValue;
+    if (a.chunk > TOK_TILE || a.sh_chunk > TOK_TILE) return hipErrorInvalidValue;
+    a.n_rt = M.rows / row_tile;
+    const dim3 grid((unsigned)((slots + N_XCD - 1) / N_XCD * N_XCD * a.n_rt));
 #define BIV_MF_CASE(KK)                                                                                         \
     if (M.cols == KK) {                                                                                         \
         k_mfma_bf16<KK, GATEUP><<<grid, NTH, 0, st>>>(a);                                                       \
