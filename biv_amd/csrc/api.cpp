@@ -380,8 +380,12 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     const bool mf_dn = T >= MFMA_MIN_T && m->down->m.ty == biv::T_BF16 && (!has_shared || m->sd->m.ty == biv::T_BF16);
     // pairs per slot: decode keeps an expert's tokens together; larger passes
     // cut them so that hot experts and the shared expert spread over the GPU
-    // (a matrix-core workgroup takes a whole slot)
-    const int chunk = mf_gu || mf_dn ? biv::MFMA_TOK_TILE : T <= 64 ? 64 : 16;
+    // (a matrix-core workgroup takes a whole slot: 256 BF16 pairs, 32 Q8_0)
+    // Q8_0 down matrices at prefill sizes run on the int8 matrix cores, when
+    // the routed and shared down matrices are Q8_0 (gate/up keeps the x86
+    // order: its outputs are quantised again)
+    const bool mq_dn = T >= MFMA_MIN_T && m->down->m.ty == biv::T_Q8_0 && (!has_shared || m->sd->m.ty == biv::T_Q8_0);
+    const int chunk = mq_dn ? biv::MFMA_Q8_TILE : mf_gu || mf_dn ? biv::MFMA_TOK_TILE : T <= 64 ? 64 : 16;
     const int u_max = biv::max_slots(ne, P, chunk);
     s.dp.slot_cap = u_max;
 
@@ -489,6 +493,9 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
             g.sh_chunk = biv::MFMA_TOK_TILE;
             HIP_TRY(ctx, biv::launch_split_bf16(s.act, has_shared ? P + T : P, ff, s.xh, s.xl, st), "split act");
             HIP_TRY(ctx, biv::launch_mfma_down(g, st), "expert down (mfma)");
+        } else if (mq_dn) {
+            d.sh_chunk = biv::MFMA_Q8_TILE;
+            HIP_TRY(ctx, biv::launch_q8_mfma_down(d, st), "expert down (int8 mfma)");
         } else {
             HIP_TRY(ctx, biv::launch_down(d, st), "expert down");
         }

@@ -99,6 +99,7 @@ struct MvArgs {
     int u_max;              // grid slots of the routed experts (max_slots)
     int n_sh;               // grid slots of the shared expert, which come first (set by the launcher)
     int sh_chunk;           // tokens per shared-expert slot (set by the launcher)
+    int n_rt;               // row tiles of a slot (matrix-core launches; set by the launcher)
 };
 
 // gate/up: out[p][r] = silu(gate_r . x) * (up_r . x) for every pair and shared row.
@@ -136,6 +137,13 @@ struct MfArgs {
 hipError_t launch_split_bf16(const float *x, int rows, int K, void *xh, void *xl, hipStream_t st);
 hipError_t launch_mfma_gateup(const MfArgs &a, hipStream_t st);
 hipError_t launch_mfma_down(const MfArgs &a, hipStream_t st);
+
+// Q8_0 down matrices at prefill sizes on the int8 matrix cores (mfma.hip):
+// the down chain kernel's contract (MvArgs: Q8 input rows a.xq / a.xd, f32
+// out, a.dump_a taps) with slots of at most MFMA_Q8_TILE pairs; routed and
+// shared down matrices all Q8_0.
+constexpr int MFMA_Q8_TILE = 32;
+hipError_t launch_q8_mfma_down(const MvArgs &a, hipStream_t st);
 
 // y = ops::rms_norm(x) of rows x n (y may be x; n a multiple of 32)
 hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, int n, float eps, hipStream_t st);

@@ -261,6 +261,185 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
             }
 }
 
+
+// ---------------------------------------------------------------------------
+// Q8_0 down matrices at prefill sizes on the int8 matrix cores.
+//
+// biv's dot_q8_0 (quant.rs:599-607, x86 1368-1382) sums, per row and input
+// row, f16(d_w) * d_x * idot over the 32-element blocks, idot the exact int32
+// dot of the block's int8 quants.  v_mfma_i32_16x16x32_i8 computes exactly
+// those int32 block dots for 16 rows x 16 pairs at once (one block per
+// instruction, so the dots stay apart); the scaling and the sum over blocks
+// run in f32 on the vector ALU, in an order of their own.  Only the down
+// matrices run here: their outputs go straight to the combine, so the other
+// order moves them by rounding only.  gate/up outputs are quantised again
+// (the down input), where a rounding difference can move a quant by one
+// step; gate/up therefore keeps the x86 order (the chain kernels).
+//
+// Operands: a block's 32 quants as lanes (x, kq) see them, kq = 0..3 taking
+// bytes 8 kq .. 8 kq + 7, for weights and activations alike.  In the chain
+// layout (layout.hpp) the 16-byte unit 16 g + 8 pi + w of a row holds word w
+// of the blocks 8 g + pi + 2 j, j = 0..3, so lane kq loads units 2 kq and
+// 2 kq + 1 of each parity (32 contiguous bytes) and finds its 8 bytes of
+// block j in word j of the two.
+//
+// A workgroup takes a slot (up to QT pairs, staged in LDS: quants and block
+// scales) and QW waves of QR rows each; a wave streams its rows' blocks from
+// HBM half a group (4 blocks of each row) ahead.  D of an MFMA: lane (n, kq)
+// holds row n, pairs 4 kq .. 4 kq + 3 of the 16-pair tile.
+constexpr int QW = 8;            // waves of a workgroup
+constexpr int QT = MFMA_Q8_TILE; // pairs of a slot (two 16-pair tiles)
+constexpr int QNTH = QW * 64;
+constexpr int QRT = 2;           // 16-row tiles of a wave
+constexpr int Q_ROWS_WG = QW * 16 * QRT;
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline float f16_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+template <int K, bool DUMP>
+__global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
+{
+    constexpr int RT = QRT;
+    constexpr int NG = K / 256; // groups of 8 blocks
+    constexpr int NB = K / 32;
+    constexpr int XSTR = K / 16 + 1; // staged quant row: 16-byte units (+1 against bank conflicts)
+    constexpr int DSTR = QT + 4;     // staged scales [block][pair], floats
+    __shared__ uint4 xq_s[QT * XSTR];
+    __shared__ float xd_s[NB * DSTR];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, kq = lane >> 4;
+    const int G = N_XCD * a.n_rt, bid = blockIdx.x;
+    const int u = (bid / G) * N_XCD + bid % N_XCD, rt = (bid % G) / N_XCD;
+    if (u >= a.u_max + a.n_sh) return;
+    const bool shared = u < a.n_sh;
+    int e = 0, beg, cnt;
+    if (shared) {
+        const int tok0 = u * a.sh_chunk;
+        beg = a.P + tok0;
+        cnt = min(a.sh_chunk, a.T - tok0);
+    } else {
+        const Slot sl = a.dp.slots[u - a.n_sh];
+        if (sl.cnt == 0) return; // uniform over the workgroup
+        e = sl.expert;
+        beg = sl.beg;
+        cnt = sl.cnt;
+    }
+    const DevMat &M = shared ? a.sa : a.a;
+    const int rows = M.rows;
+    // the weight rows of this lane: row n of each 16-row tile
+    const int rw0 = rt * Q_ROWS_WG + wave * 16 * RT;
+    const uint4 *wq[RT];
+    const uint2 *wsc[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const size_t row = (size_t)e * rows + rw0 + 16 * r + n;
+        wq[r] = reinterpret_cast<const uint4 *>(M.q + row * K) + 2 * kq;
+        wsc[r] = reinterpret_cast<const uint2 *>(M.s + row * NB * 2);
+    }
+    // half-group h = (g, pi)'s weights: per tile two units of quants and 4
+    // f16 scales (blocks 8 g + pi + 2 j)
+    struct Half {
+        uint4 q[RT][2];
+        uint2 s[RT];
+    };
+    auto load = [&](int h, Half &w) {
+        const int g = h >> 1, pi = h & 1;
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            w.q[r][0] = wq[r][16 * g + 8 * pi];
+            w.q[r][1] = wq[r][16 * g + 8 * pi + 1];
+            w.s[r] = wsc[r][(pi * (K / 64) + 4 * g) / 4];
+        }
+    };
+    Half w0, w1;
+    load(0, w0); // the first weights go out before the staging waits
+    // stage the slot's input rows: quants (chain layout, row stride XSTR
+    // units) and block scales transposed to [block][pair]; pairs past the
+    // count repeat the last one (their results are not stored)
+    {
+        constexpr int UPR = K / 16; // units per row
+        static_assert((QT * UPR) % QNTH == 0, "staging shape");
+#pragma unroll
+        for (int it = 0; it < QT * UPR / QNTH; it++) {
+            const int idx = tid + QNTH * it, i = idx / UPR, c = idx % UPR;
+            const size_t ar = beg + min(i, cnt - 1);
+            xq_s[i * XSTR + c] = reinterpret_cast<const uint4 *>(a.xq + ar * K)[c];
+        }
+        for (int idx = tid; idx < QT * NB; idx += QNTH) {
+            const int i = idx / NB, bs = idx % NB;
+            const size_t ar = beg + min(i, cnt - 1);
+            const int b = 2 * (bs % (K / 64)) + bs / (K / 64); // lay::q8_scale's inverse
+            xd_s[b * DSTR + i] = a.xd[ar * NB + bs];
+        }
+    }
+    __syncthreads();
+    const bool live1 = cnt > 16; // the second 16-pair tile holds pairs
+    float acc[2][RT][4];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[t][r][j] = 0.0f;
+    auto compute = [&](int h, const Half &w) {
+        const int g = h >> 1, pi = h & 1;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            if (t == 1 && !live1) break;
+            // this lane's activation units of the half-group
+            const uint4 *xr = xq_s + (16 * t + n) * XSTR + 16 * g + 8 * pi + 2 * kq;
+            const uint4 x0 = xr[0], x1 = xr[1];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int b = 8 * g + pi + 2 * j;
+                const float4 dx = *reinterpret_cast<const float4 *>(xd_s + b * DSTR + 16 * t + 4 * kq);
+                const long xo = (long)((uint64_t)x0[j] | (uint64_t)x1[j] << 32);
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    const uint32_t h2 = j < 2 ? w.s[r].x : w.s[r].y;
+                    const float dw = f16_to_f32((j & 1) ? h2 >> 16 : h2 & 0xFFFF);
+                    const long wo = (long)((uint64_t)w.q[r][0][j] | (uint64_t)w.q[r][1][j] << 32);
+                    const i32x4 z = {0, 0, 0, 0};
+                    const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo, wo, z, 0, 0, 0);
+                    acc[t][r][0] = __builtin_fmaf((float)d[0], dx.x * dw, acc[t][r][0]);
+                    acc[t][r][1] = __builtin_fmaf((float)d[1], dx.y * dw, acc[t][r][1]);
+                    acc[t][r][2] = __builtin_fmaf((float)d[2], dx.z * dw, acc[t][r][2]);
+                    acc[t][r][3] = __builtin_fmaf((float)d[3], dx.w * dw, acc[t][r][3]);
+                    if (DUMP && a.dump_a) { // the block dots, for the taps
+#pragma unroll
+                        for (int jj = 0; jj < 4; jj++) {
+                            const int i = 16 * t + 4 * kq + jj;
+                            if (i < cnt) a.dump_a[((size_t)(beg + i) * rows + rw0 + 16 * r + n) * NB + b] = d[jj];
+                        }
+                    }
+                }
+                // keep each block's MFMA results short-lived (registers for
+                // more waves rather than for MFMAs in flight)
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+    // two half-groups per turn, loads one ahead
+    for (int h = 0; h < 2 * NG; h += 2) {
+        load(h + 1, w1);
+        compute(h, w0);
+        if (h + 2 < 2 * NG) load(h + 2, w0);
+        compute(h + 1, w1);
+    }
+    // pair 16 t + 4 kq + j of the slot, row rw0 + 16 r + n
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = 16 * t + 4 * kq + j;
+            if (i < cnt) {
+#pragma unroll
+                for (int r = 0; r < RT; r++) a.out[(size_t)(beg + i) * rows + rw0 + 16 * r + n] = acc[t][r][j];
+            }
+        }
+}
+
 } // namespace
 
 hipError_t launch_split_bf16(const float *x, int rows, int K, void *xh, void *xl, hipStream_t st)
@@ -309,5 +488,40 @@ template <bool GATEUP> hipError_t launch_mfma(const MfArgs &a, hipStream_t st)
 
 hipError_t launch_mfma_gateup(const MfArgs &a, hipStream_t st) { return launch_mfma<true>(a, st); }
 hipError_t launch_mfma_down(const MfArgs &a, hipStream_t st) { return launch_mfma<false>(a, st); }
+
+
+hipError_t launch_q8_down_t(MvArgs a, int routed, int shared, hipStream_t st)
+{
+    const DevMat &M = routed ? a.a : a.sa;
+    if (!routed) a.u_max = 0;
+    a.n_sh = shared ? (a.T + a.sh_chunk - 1) / a.sh_chunk : 0;
+    const int slots = a.u_max + a.n_sh;
+    if (slots == 0) return hipSuccess;
+    if (a.sh_chunk > QT || M.rows % Q_ROWS_WG) return hipErrorInvalidValue;
+    a.n_rt = M.rows / Q_ROWS_WG;
+    const dim3 grid((unsigned)((slots + N_XCD - 1) / N_XCD * N_XCD * a.n_rt));
+#define BIV_Q8_CASE(KK)                                                                                         \
+    if (M.cols == KK) {                                                                                         \
+        if (a.dump_a)                                                                                           \
+            k_q8_down_mfma<KK, true><<<grid, QNTH, 0, st>>>(a);                                                 \
+        else                                                                                                    \
+            k_q8_down_mfma<KK, false><<<grid, QNTH, 0, st>>>(a);                                                \
+        return hipGetLastError();                                                                               \
+    }
+    BIV_Q8_CASE(2048)
+    BIV_Q8_CASE(1024)
+    BIV_Q8_CASE(512)
+#undef BIV_Q8_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_q8_mfma_down(const MvArgs &a, hipStream_t st)
+{
+    const bool has_shared = a.sa.q != nullptr;
+    if (has_shared && a.sa.cols == a.a.cols && a.sa.rows == a.a.rows) return launch_q8_down_t(a, 1, 1, st);
+    hipError_t err = launch_q8_down_t(a, 1, 0, st);
+    if (err != hipSuccess || !has_shared) return err;
+    return launch_q8_down_t(a, 0, 1, st);
+}
 
 } // namespace biv

@@ -119,12 +119,16 @@ def full_parity(orc, engine, layer, moe, h, block_dots=True, min_exact=0.9999):
 @pytest.mark.parametrize("T", [1, 2, 5, 9, 64, 65, 100])
 def test_q8_small_layer(orc, engine, T):
     """T <= 16 quantises the SwiGLU intermediate inside the down kernel,
-    larger T in its own launch; T > 64 cuts an expert's pairs into slots of
-    16.  All must give the oracle's bits."""
+    larger T in its own launch; below 64 every sum runs in the x86 order and
+    the outputs carry the oracle's bits.  From T = 64 the experts run on the
+    int8 matrix cores (slots of 32 pairs): the int32 block dots are still the
+    oracle's exactly (checked from the MFMA kernel's own taps), the f32 sums
+    over blocks run in another order, so the outputs meet the tolerance."""
     print(f"case q8 small T={T}", flush=True)
     layer, moe = layer_for(engine, seed=21, n_expert=32)
     h = synth.make_tokens(100 + T, T, offsets=True)
-    full_parity(orc, engine, layer, moe, h, block_dots=T <= 9)
+    full_parity(orc, engine, layer, moe, h, block_dots=T <= 9 or T in (64, 65),
+                min_exact=0.9999 if T < 64 else 0.0)
 
 
 @pytest.mark.parametrize("T", [1, 5, 40])
@@ -149,7 +153,7 @@ def test_q8_prefill_zipf_512(orc, engine, skew):
     got, t = moe.ffn_taps(h, dots=False)
     assert np.array_equal(t["ids"], ids)
     check_dispatch(t, ids, 512, layer.k)
-    check_output(ref, got)
+    check_output(ref, got, min_exact=0.0)  # int8 MFMA: f32 block sums in their own order
     again = moe.ffn(h)
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
 
