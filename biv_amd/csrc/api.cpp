@@ -380,12 +380,13 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     const bool mf_dn = T >= MFMA_MIN_T && m->down->m.ty == biv::T_BF16 && (!has_shared || m->sd->m.ty == biv::T_BF16);
     // pairs per slot: decode keeps an expert's tokens together; larger passes
     // cut them so that hot experts and the shared expert spread over the GPU
-    // (a matrix-core workgroup takes a whole slot: 256 BF16 pairs, 32 Q8_0)
-    // Q8_0 down matrices at prefill sizes run on the int8 matrix cores, when
-    // the routed and shared down matrices are Q8_0 (gate/up keeps the x86
-    // order: its outputs are quantised again)
+    // (a matrix-core workgroup takes a whole slot: 256 BF16 pairs, 16 Q8_0)
+    // Q8_0 matrices at prefill sizes run on the int8 matrix cores, when the
+    // routed and shared matrices of that half are all Q8_0
+    const bool mq_gu = T >= MFMA_MIN_T && m->gate->m.ty == biv::T_Q8_0 && m->up->m.ty == biv::T_Q8_0 &&
+                       (!has_shared || (m->sg->m.ty == biv::T_Q8_0 && m->su->m.ty == biv::T_Q8_0));
     const bool mq_dn = T >= MFMA_MIN_T && m->down->m.ty == biv::T_Q8_0 && (!has_shared || m->sd->m.ty == biv::T_Q8_0);
-    const int chunk = mq_dn ? biv::MFMA_Q8_TILE : mf_gu || mf_dn ? biv::MFMA_TOK_TILE : T <= 64 ? 64 : 16;
+    const int chunk = mq_gu || mq_dn ? biv::MFMA_Q8_TILE : mf_gu || mf_dn ? biv::MFMA_TOK_TILE : T <= 64 ? 64 : 16;
     const int u_max = biv::max_slots(ne, P, chunk);
     s.dp.slot_cap = u_max;
 
@@ -443,6 +444,9 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
             g.sh_chunk = biv::MFMA_TOK_TILE;
             HIP_TRY(ctx, biv::launch_split_bf16(h, T, E, s.xh, s.xl, st), "split h");
             HIP_TRY(ctx, biv::launch_mfma_gateup(g, st), "expert gate/up (mfma)");
+        } else if (mq_gu) {
+            a.sh_chunk = biv::MFMA_Q8_TILE;
+            HIP_TRY(ctx, biv::launch_q8_mfma_gateup(a, st), "expert gate/up (int8 mfma)");
         } else {
             HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
         }

@@ -12,6 +12,8 @@
 // 128 (c / 16) + 16 m + (c % 16), m = 0..7: the BF16 weight layout of
 // layout.hpp (bf16_elem), so a lane's MFMA operand is one 16-byte load of the
 // weights and one of each activation half.
+#include <type_traits>
+
 #include "common.hpp"
 #include "expf_ref.h"
 
@@ -288,7 +290,8 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 // HBM half a group (4 blocks of each row) ahead.  D of an MFMA: lane (n, kq)
 // holds row n, pairs 4 kq .. 4 kq + 3 of the 16-pair tile.
 constexpr int QW = 8;            // waves of a workgroup
-constexpr int QT = MFMA_Q8_TILE; // pairs of a slot (two 16-pair tiles)
+constexpr int QT = MFMA_Q8_TILE; // pairs of a slot
+constexpr int NTT = QT / 16;     // 16-pair tiles of a slot
 constexpr int QNTH = QW * 64;
 constexpr int QRT = 2;           // 16-row tiles of a wave
 constexpr int Q_ROWS_WG = QW * 16 * QRT;
@@ -374,10 +377,9 @@ __global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
         }
     }
     __syncthreads();
-    const bool live1 = cnt > 16; // the second 16-pair tile holds pairs
-    float acc[2][RT][4];
+    float acc[NTT][RT][4];
 #pragma unroll
-    for (int t = 0; t < 2; t++)
+    for (int t = 0; t < NTT; t++)
 #pragma unroll
         for (int r = 0; r < RT; r++)
 #pragma unroll
@@ -385,8 +387,8 @@ __global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
     auto compute = [&](int h, const Half &w) {
         const int g = h >> 1, pi = h & 1;
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            if (t == 1 && !live1) break;
+        for (int t = 0; t < NTT; t++) {
+            if (16 * t >= cnt) break; // uniform: no pairs in this tile
             // this lane's activation units of the half-group
             const uint4 *xr = xq_s + (16 * t + n) * XSTR + 16 * g + 8 * pi + 2 * kq;
             const uint4 x0 = xr[0], x1 = xr[1];
@@ -429,7 +431,7 @@ __global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
     }
     // pair 16 t + 4 kq + j of the slot, row rw0 + 16 r + n
 #pragma unroll
-    for (int t = 0; t < 2; t++)
+    for (int t = 0; t < NTT; t++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int i = 16 * t + 4 * kq + j;
@@ -438,6 +440,186 @@ __global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
                 for (int r = 0; r < RT; r++) a.out[(size_t)(beg + i) * rows + rw0 + 16 * r + n] = acc[t][r][j];
             }
         }
+}
+
+
+// ---------------------------------------------------------------------------
+// Q8_0 gate/up at prefill sizes, bit for bit in the x86 order, with the
+// integer work on the matrix cores.
+//
+// biv's x86 dot_q8_0 (quant.rs:1368-1382) keeps 16 f32 chains per row: chain
+// (pi, l) takes the blocks b = pi, pi + 2, ... and for each the int32 of the
+// block's word l (bytes 4l..4l+3: a 4-element dot), fma(float(word dot),
+// f16(d_w) * d_x, acc); then the chains are summed in a fixed tree (the
+// chain kernels in kernels.hip do exactly this on the vector ALU).  Here
+// v_mfma_i32_16x16x32_i8 produces the word dots: its A operand is the block
+// of two input rows, masked so that A row 8 tt + l keeps only word l of
+// input row tt; its B operand is the block of 16 weight rows (8 gate rows,
+// then the same 8 rows of up).  D row 8 tt + l, column n is then the word-l
+// dot of input row tt and weight row n, exactly.  The vector ALU does what
+// remains, in the reference's order: convert, fma into the chain, tree.
+//
+// D of an MFMA: lane (n, kq) holds column n and A rows 4 kq .. 4 kq + 3,
+// i.e. input row kq / 2 of the pair, words 4 (kq & 1) .. + 3: eight chains
+// (two parities x four words) of one (input row, weight row); the other
+// eight are in lane (n, kq ^ 1).
+//
+// A workgroup takes a slot (up to QT pairs, MFMA_Q8_TILE, staged in LDS)
+// and QW waves of 8 output rows; a wave streams its 16 weight rows half a
+// group ahead and keeps the chains of all pairs of the slot in registers.
+template <int K, bool DUMP>
+__global__ __launch_bounds__(QNTH) void k_q8_gu_exact(MvArgs a)
+{
+    constexpr int NG = K / 256; // groups of 8 blocks
+    constexpr int NB = K / 32;
+    constexpr int NPR = QT / 2;      // input-row pairs of a slot
+    constexpr int XSTR = K / 16 + 1; // staged quant row: 16-byte units (+1 against bank conflicts)
+    constexpr int DSTR = NB + 4;     // staged scales [pair][block]: floats (16-byte aligned rows)
+    static_assert(QT % 2 == 0, "pairs of input rows");
+    __shared__ uint4 xq_s[QT * XSTR];
+    __shared__ float xd_s[QT * DSTR];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, kq = lane >> 4;
+    const int G = N_XCD * a.n_rt, bid = blockIdx.x;
+    const int u = (bid / G) * N_XCD + bid % N_XCD, rt = (bid % G) / N_XCD;
+    if (u >= a.u_max + a.n_sh) return;
+    const bool shared = u < a.n_sh;
+    int e = 0, beg, cnt, tok0 = 0;
+    if (shared) {
+        tok0 = u * a.sh_chunk;
+        beg = a.P + tok0;
+        cnt = min(a.sh_chunk, a.T - tok0);
+    } else {
+        const Slot sl = a.dp.slots[u - a.n_sh];
+        if (sl.cnt == 0) return; // uniform over the workgroup
+        e = sl.expert;
+        beg = sl.beg;
+        cnt = sl.cnt;
+    }
+    DevMat M = shared ? a.sa : a.a;
+    const DevMat &B = shared ? a.sb : a.b;
+    const int rows = M.rows;
+    // this lane's weight row: column n of the MFMA tile, gate rows then up
+    const int orow = rt * (QW * 8) + wave * 8 + (n & 7);
+    const uint8_t *mq = n < 8 ? M.q : B.q, *ms = n < 8 ? M.s : B.s;
+    const size_t wr = (size_t)e * rows + orow;
+    const uint4 *wq = reinterpret_cast<const uint4 *>(mq + wr * K) + 2 * kq;
+    const uint2 *wsc = reinterpret_cast<const uint2 *>(ms + wr * NB * 2);
+    // half-group h = (g, pi): units 2 kq, 2 kq + 1 of the row and the 4 f16
+    // scales of blocks 8 g + pi + 2 j
+    struct Half {
+        uint4 q[2];
+        uint2 s;
+    };
+    auto load = [&](int h, Half &w) {
+        const int g = h >> 1, pi = h & 1;
+        w.q[0] = wq[16 * g + 8 * pi];
+        w.q[1] = wq[16 * g + 8 * pi + 1];
+        w.s = wsc[(pi * (K / 64) + 4 * g) / 4];
+    };
+    Half w0, w1;
+    load(0, w0); // the first weights go out before the staging waits
+    // stage the slot's input rows: quants (chain layout, row stride XSTR
+    // units) and block scales [row][q8_scale order]; rows past the count
+    // repeat the last one (their results are not stored)
+    {
+        constexpr int UPR = K / 16; // units per row
+        for (int idx = tid; idx < QT * UPR; idx += QNTH) {
+            const int i = idx / UPR, c = idx % UPR;
+            const int ti = min(i, cnt - 1);
+            const size_t ar = shared ? (size_t)(tok0 + ti) : (size_t)a.dp.pair_tok[beg + ti];
+            xq_s[i * XSTR + c] = reinterpret_cast<const uint4 *>(a.xq + ar * K)[c];
+        }
+        for (int idx = tid; idx < QT * NB; idx += QNTH) {
+            const int i = idx / NB, bs = idx % NB;
+            const int ti = min(i, cnt - 1);
+            const size_t ar = shared ? (size_t)(tok0 + ti) : (size_t)a.dp.pair_tok[beg + ti];
+            xd_s[i * DSTR + bs] = a.xd[ar * NB + bs];
+        }
+    }
+    __syncthreads();
+    const int npairs = (cnt + 1) / 2;
+    // the A operand's mask: A row 8 tt + l keeps word l, which lane kq holds
+    // as word 0 (l = 2 kq) or word 1 (l = 2 kq + 1) of its 8 bytes
+    const int tt = (n >> 3), l = n & 7;
+    const uint32_t keep0 = l == 2 * kq ? ~0u : 0u, keep1 = l == 2 * kq + 1 ? ~0u : 0u;
+    // this lane's D: input row kq / 2 of the pair, chains (pi, 4 (kq & 1) + jj)
+    const int drow = kq >> 1;
+    float acc[NPR][2][4];
+#pragma unroll
+    for (int p = 0; p < NPR; p++)
+#pragma unroll
+        for (int pi = 0; pi < 2; pi++)
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) acc[p][pi][jj] = 0.0f;
+    // pi a compile-time constant: it picks the chain accumulators
+    auto compute = [&](int g, auto pi_c, const Half &w) {
+        constexpr int pi = decltype(pi_c)::value;
+        // the weight row's 4 block scales as f32
+        float dw[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t h2 = j < 2 ? w.s.x : w.s.y;
+            dw[j] = f16_to_f32((j & 1) ? h2 >> 16 : h2 & 0xFFFF);
+        }
+#pragma unroll
+        for (int p = 0; p < NPR; p++) {
+            if (2 * p < cnt) { // uniform
+            // A: input row 2 p + tt's units 2 kq, 2 kq + 1 of the half-group
+            const uint4 *xr = xq_s + (2 * p + tt) * XSTR + 16 * g + 8 * pi + 2 * kq;
+            const uint4 x0 = xr[0], x1 = xr[1];
+            // d_x of the 4 blocks for this lane's D row (input row 2 p + drow)
+            const float4 dx = *reinterpret_cast<const float4 *>(xd_s + (2 * p + drow) * DSTR + pi * (K / 64) + 4 * g);
+            const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t lo = x0[j] & keep0, hi = x1[j] & keep1;
+                const long xo = (long)((uint64_t)lo | (uint64_t)hi << 32);
+                const long wo = (long)((uint64_t)w.q[0][j] | (uint64_t)w.q[1][j] << 32);
+                const i32x4 z = {0, 0, 0, 0};
+                const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo, wo, z, 0, 0, 0);
+                const float sb = dw[j] * dxs[j]; // f16(d_w) * d_x, as the reference
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) acc[p][pi][jj] = __builtin_fmaf((float)d[jj], sb, acc[p][pi][jj]);
+                if (DUMP) {
+                    // the block's int32: the sum of its 8 word dots
+                    int bs = d[0] + d[1] + d[2] + d[3];
+                    bs += __shfl_xor(bs, 16);
+                    int32_t *dump = n < 8 ? a.dump_a : a.dump_b;
+                    const int i = 2 * p + drow;
+                    if (dump && !(kq & 1) && i < cnt)
+                        dump[((size_t)(beg + i) * rows + orow) * NB + 8 * g + pi + 2 * j] = bs;
+                }
+            }
+            }
+            // one pair's LDS reads and MFMA results live at a time
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // two half-groups per turn, loads one ahead
+    for (int h = 0; h < 2 * NG; h += 2) {
+        load(h + 1, w1);
+        compute(h >> 1, std::integral_constant<int, 0>(), w0);
+        if (h + 2 < 2 * NG) load(h + 2, w0);
+        compute(h >> 1, std::integral_constant<int, 1>(), w1);
+    }
+    // the reference's tree: u_l = chain (0, l) + chain (1, l); v = u_l +
+    // u_(l+4) (the lane with kq ^ 1 holds words 4..7); (v0 + v2) + (v1 + v3);
+    // then silu(gate) * up, up from column n + 8
+#pragma unroll
+    for (int p = 0; p < NPR; p++) {
+        if (2 * p >= cnt) break;
+        float v[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            const float uu = acc[p][0][jj] + acc[p][1][jj];
+            v[jj] = uu + __shfl_xor(uu, 16);
+        }
+        const float t = (v[0] + v[2]) + (v[1] + v[3]);
+        const float up = __shfl_xor(t, 8);
+        const int i = 2 * p + drow;
+        if (n < 8 && !(kq & 1) && i < cnt) a.out[(size_t)(beg + i) * rows + orow] = silu_mul_t(t, up, exp_tab);
+    }
 }
 
 } // namespace
@@ -522,6 +704,41 @@ hipError_t launch_q8_mfma_down(const MvArgs &a, hipStream_t st)
     hipError_t err = launch_q8_down_t(a, 1, 0, st);
     if (err != hipSuccess || !has_shared) return err;
     return launch_q8_down_t(a, 0, 1, st);
+}
+
+
+hipError_t launch_q8_gu_t(MvArgs a, int routed, int shared, hipStream_t st)
+{
+    const DevMat &M = routed ? a.a : a.sa;
+    if (!routed) a.u_max = 0;
+    a.n_sh = shared ? (a.T + a.sh_chunk - 1) / a.sh_chunk : 0;
+    const int slots = a.u_max + a.n_sh;
+    if (slots == 0) return hipSuccess;
+    if (a.sh_chunk > QT || M.rows % (QW * 8)) return hipErrorInvalidValue;
+    a.n_rt = M.rows / (QW * 8);
+    const dim3 grid((unsigned)((slots + N_XCD - 1) / N_XCD * N_XCD * a.n_rt));
+#define BIV_Q8_CASE(KK)                                                                                         \
+    if (M.cols == KK) {                                                                                         \
+        if (a.dump_a || a.dump_b)                                                                               \
+            k_q8_gu_exact<KK, true><<<grid, QNTH, 0, st>>>(a);                                                  \
+        else                                                                                                    \
+            k_q8_gu_exact<KK, false><<<grid, QNTH, 0, st>>>(a);                                                 \
+        return hipGetLastError();                                                                               \
+    }
+    BIV_Q8_CASE(2048)
+    BIV_Q8_CASE(1024)
+    BIV_Q8_CASE(512)
+#undef BIV_Q8_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_q8_mfma_gateup(const MvArgs &a, hipStream_t st)
+{
+    const bool has_shared = a.sa.q != nullptr;
+    if (has_shared && a.sa.cols == a.a.cols && a.sa.rows == a.a.rows) return launch_q8_gu_t(a, 1, 1, st);
+    hipError_t err = launch_q8_gu_t(a, 1, 0, st);
+    if (err != hipSuccess || !has_shared) return err;
+    return launch_q8_gu_t(a, 0, 1, st);
 }
 
 } // namespace biv
