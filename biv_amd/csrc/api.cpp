@@ -381,11 +381,14 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     // pairs per slot: decode keeps an expert's tokens together; larger passes
     // cut them so that hot experts and the shared expert spread over the GPU
     // (a matrix-core workgroup takes a whole slot: 256 BF16 pairs, 16 Q8_0)
-    // Q8_0 matrices at prefill sizes run on the int8 matrix cores, when the
-    // routed and shared matrices of that half are all Q8_0
-    const bool mq_gu = T >= MFMA_MIN_T && m->gate->m.ty == biv::T_Q8_0 && m->up->m.ty == biv::T_Q8_0 &&
-                       (!has_shared || (m->sg->m.ty == biv::T_Q8_0 && m->su->m.ty == biv::T_Q8_0));
-    const bool mq_dn = T >= MFMA_MIN_T && m->down->m.ty == biv::T_Q8_0 && (!has_shared || m->sd->m.ty == biv::T_Q8_0);
+    // quantised matrices at prefill sizes run on the int8 matrix cores: gate/up
+    // when gate and up are Q8_0 or Q4_K (each pair of one type, routed and
+    // shared), down when the routed and shared down matrices are Q8_0 or Q6_K
+    auto gu_ok = [](int g, int u) { return g == u && (g == biv::T_Q8_0 || g == biv::T_Q4K); };
+    const bool mq_gu = T >= MFMA_MIN_T && gu_ok(m->gate->m.ty, m->up->m.ty) &&
+                       (!has_shared || gu_ok(m->sg->m.ty, m->su->m.ty));
+    auto dn_ok = [](int t) { return t == biv::T_Q8_0 || t == biv::T_Q6K; };
+    const bool mq_dn = T >= MFMA_MIN_T && dn_ok(m->down->m.ty) && (!has_shared || dn_ok(m->sd->m.ty));
     const int chunk = mq_gu || mq_dn ? biv::MFMA_Q8_TILE : mf_gu || mf_dn ? biv::MFMA_TOK_TILE : T <= 64 ? 64 : 16;
     const int u_max = biv::max_slots(ne, P, chunk);
     s.dp.slot_cap = u_max;
@@ -446,7 +449,7 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
             HIP_TRY(ctx, biv::launch_mfma_gateup(g, st), "expert gate/up (mfma)");
         } else if (mq_gu) {
             a.sh_chunk = biv::MFMA_Q8_TILE;
-            HIP_TRY(ctx, biv::launch_q8_mfma_gateup(a, st), "expert gate/up (int8 mfma)");
+            HIP_TRY(ctx, biv::launch_mfma_gateup_exact(a, st), "expert gate/up (int8 mfma)");
         } else {
             HIP_TRY(ctx, biv::launch_gateup(a, st), "expert gate/up");
         }

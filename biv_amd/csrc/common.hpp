@@ -138,14 +138,15 @@ hipError_t launch_split_bf16(const float *x, int rows, int K, void *xh, void *xl
 hipError_t launch_mfma_gateup(const MfArgs &a, hipStream_t st);
 hipError_t launch_mfma_down(const MfArgs &a, hipStream_t st);
 
-// Q8_0 experts at prefill sizes on the int8 matrix cores (mfma.hip), with
-// the chain kernels' contract (MvArgs: Q8 input rows a.xq / a.xd, f32 out,
-// dump taps) and slots of at most MFMA_Q8_TILE pairs; routed and shared
-// matrices of the half all Q8_0.  gate/up: bit for bit the x86 order (the
-// MFMAs make the 4-element word dots); down: exact int32 block dots, f32
-// sums over blocks in an order of their own.
+// Quantised experts at prefill sizes on the int8 matrix cores (mfma.hip),
+// with the chain kernels' contract (MvArgs: Q8 input rows a.xq / a.xd / a.xs,
+// f32 out, dump taps) and slots of at most MFMA_Q8_TILE pairs.  gate/up
+// (Q8_0 or Q4_K; gate and up of one type): bit for bit the x86 order, the
+// MFMAs making the 4-element word dots.  down (Q8_0 or Q6_K):
+// exact int32 block dots (Q6_K: 16-element halves times their sub-scales),
+// f32 sums over blocks in an order of their own.
 constexpr int MFMA_Q8_TILE = 16;
-hipError_t launch_q8_mfma_gateup(const MvArgs &a, hipStream_t st);
+hipError_t launch_mfma_gateup_exact(const MvArgs &a, hipStream_t st);
 hipError_t launch_q8_mfma_down(const MvArgs &a, hipStream_t st);
 
 // y = ops::rms_norm(x) of rows x n (y may be x; n a multiple of 32)

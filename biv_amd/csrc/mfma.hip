@@ -16,6 +16,7 @@
 
 #include "common.hpp"
 #include "expf_ref.h"
+#include "layout.hpp"
 
 namespace biv {
 namespace {
@@ -300,6 +301,13 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 __device__ inline float f16_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
+// byte i (0..15) of a 16-byte vector
+__device__ inline int byte_at4(const int4 &v, int i)
+{
+    const int w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
+    return ((unsigned)w >> (8 * (i & 3))) & 0xFF;
+}
+
 template <int K, bool DUMP>
 __global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
 {
@@ -444,20 +452,22 @@ __global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
 
 
 // ---------------------------------------------------------------------------
-// Q8_0 gate/up at prefill sizes, bit for bit in the x86 order, with the
-// integer work on the matrix cores.
+// Q8_0 and Q4_K gate/up at prefill sizes, bit for bit in the x86 order, with
+// the integer work on the matrix cores.
 //
-// biv's x86 dot_q8_0 (quant.rs:1368-1382) keeps 16 f32 chains per row: chain
-// (pi, l) takes the blocks b = pi, pi + 2, ... and for each the int32 of the
-// block's word l (bytes 4l..4l+3: a 4-element dot), fma(float(word dot),
-// f16(d_w) * d_x, acc); then the chains are summed in a fixed tree (the
-// chain kernels in kernels.hip do exactly this on the vector ALU).  Here
+// biv's x86 dot_q8_0 and dot_q4k (quant.rs:1368-1423) keep 16 f32 chains per
+// row: chain (pi, l) takes the 32-element blocks b = pi, pi + 2, ... and for
+// each the int32 of the block's word l (bytes 4l..4l+3: a 4-element dot),
+// fma(float(word dot), w_scale(b) * d_x(b), acc); then the chains are summed
+// in a fixed tree, and Q4_K subtracts its mins term last (the chain kernels
+// in kernels.hip do exactly this on the vector ALU).  Here
 // v_mfma_i32_16x16x32_i8 produces the word dots: its A operand is the block
 // of two input rows, masked so that A row 8 tt + l keeps only word l of
 // input row tt; its B operand is the block of 16 weight rows (8 gate rows,
-// then the same 8 rows of up).  D row 8 tt + l, column n is then the word-l
-// dot of input row tt and weight row n, exactly.  The vector ALU does what
-// remains, in the reference's order: convert, fma into the chain, tree.
+// then the same 8 rows of up) as int8 (Q4_K: the block's nibbles, 0..15).
+// D row 8 tt + l, column n is then the word-l dot of input row tt and weight
+// row n, exactly.  The vector ALU does what remains, in the reference's
+// order: convert, fma into the chain, tree, mins, SwiGLU.
 //
 // D of an MFMA: lane (n, kq) holds column n and A rows 4 kq .. 4 kq + 3,
 // i.e. input row kq / 2 of the pair, words 4 (kq & 1) .. + 3: eight chains
@@ -465,19 +475,97 @@ __global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
 // eight are in lane (n, kq ^ 1).
 //
 // A workgroup takes a slot (up to QT pairs, MFMA_Q8_TILE, staged in LDS)
-// and QW waves of 8 output rows; a wave streams its 16 weight rows half a
-// group ahead and keeps the chains of all pairs of the slot in registers.
-template <int K, bool DUMP>
-__global__ __launch_bounds__(QNTH) void k_q8_gu_exact(MvArgs a)
+// and QW waves of 8 output rows; a wave streams its 16 weight rows a step
+// ahead and keeps the chains of all pairs of the slot in registers.
+
+// Weight operands of the exact kernel.  A step covers the blocks 8 g + pi +
+// 2 j (j = 0..3) of one parity (Q8_0: a half-group) or both parities (Q4_K:
+// super-block g, whose nibble bytes serve both).  operand(w, pi, j) is the
+// lane's 8 bytes of block 8 g + pi + 2 j; scale(w, pi, j) its f32 weight
+// scale as the reference forms it.
+template <int TY, int K> struct GuW;
+
+// Q8_0 (chain layout: unit 16 g + 8 pi + w holds word w of the blocks
+// 8 g + pi + 2 j); scale f16(d) (quant.rs:1368-1382)
+template <int K> struct GuW<T_Q8_0, K> {
+    static constexpr int STEPS = K / 128; // half-groups
+    static constexpr bool BOTH = false;  // a step is one parity
+    struct Step {
+        uint4 q[2];
+        uint2 s;
+    };
+    const uint4 *wq;
+    const uint2 *wsc;
+    __device__ GuW(const uint8_t *q, const uint8_t *s, size_t row, int kq)
+        : wq(reinterpret_cast<const uint4 *>(q + row * K) + 2 * kq),
+          wsc(reinterpret_cast<const uint2 *>(s + row * (K / 32) * 2)) {}
+    __device__ void load(int h, Step &w) const
+    {
+        const int g = h >> 1, pi = h & 1;
+        w.q[0] = wq[16 * g + 8 * pi];
+        w.q[1] = wq[16 * g + 8 * pi + 1];
+        w.s = wsc[(pi * (K / 64) + 4 * g) / 4];
+    }
+    __device__ static long operand(const Step &w, int pi, int j)
+    {
+        return (long)((uint64_t)w.q[0][j] | (uint64_t)w.q[1][j] << 32);
+    }
+    __device__ static float scale(const Step &w, int pi, int j)
+    {
+        const uint32_t h2 = j < 2 ? w.s.x : w.s.y;
+        return f16_to_f32((j & 1) ? h2 >> 16 : h2 & 0xFFFF);
+    }
+};
+
+// Q4_K (chain layout: unit 8 g + w holds word w of the four sub-block pairs
+// of super-block g, low nibbles the even sub-block, high the odd); scale
+// d * sc of the sub-block, the mins apart (quant.rs:1384-1423)
+template <int K> struct GuW<T_Q4K, K> {
+    static constexpr int STEPS = K / 256; // super-blocks
+    static constexpr bool BOTH = true;
+    struct Step {
+        uint4 q[2];
+        int4 hd; // d, dmin, the 12 scale bytes
+    };
+    const uint4 *wq;
+    const int4 *whd;
+    __device__ GuW(const uint8_t *q, const uint8_t *s, size_t row, int kq)
+        : wq(reinterpret_cast<const uint4 *>(q + row * (K / 2)) + 2 * kq),
+          whd(reinterpret_cast<const int4 *>(s + row * (K / 256) * 16)) {}
+    __device__ void load(int g, Step &w) const
+    {
+        w.q[0] = wq[8 * g];
+        w.q[1] = wq[8 * g + 1];
+        w.hd = whd[g];
+    }
+    __device__ static long operand(const Step &w, int pi, int j)
+    {
+        const uint32_t lo = (w.q[0][j] >> (4 * pi)) & 0x0F0F0F0Fu, hi = (w.q[1][j] >> (4 * pi)) & 0x0F0F0F0Fu;
+        return (long)((uint64_t)lo | (uint64_t)hi << 32);
+    }
+    __device__ static float scale(const Step &w, int pi, int j)
+    {
+        const int sb = 2 * j + pi;
+        const int sc = sb < 4 ? byte_at4(w.hd, 4 + sb) & 63
+                              : (byte_at4(w.hd, 4 + sb + 4) & 0xF) | ((byte_at4(w.hd, 4 + sb - 4) >> 6) << 4);
+        const float d = f16_to_f32((uint32_t)w.hd.x & 0xFFFF);
+        return d * (float)sc;
+    }
+};
+
+template <int TY, int K, bool DUMP>
+__global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
 {
-    constexpr int NG = K / 256; // groups of 8 blocks
+    using W = GuW<TY, K>;
     constexpr int NB = K / 32;
     constexpr int NPR = QT / 2;      // input-row pairs of a slot
     constexpr int XSTR = K / 16 + 1; // staged quant row: 16-byte units (+1 against bank conflicts)
-    constexpr int DSTR = NB + 4;     // staged scales [pair][block]: floats (16-byte aligned rows)
+    constexpr int DSTR = NB + 4;     // staged scales [row][q8_scale order]: floats (16-byte aligned rows)
+    constexpr bool Q4K = TY == T_Q4K;
     static_assert(QT % 2 == 0, "pairs of input rows");
     __shared__ uint4 xq_s[QT * XSTR];
     __shared__ float xd_s[QT * DSTR];
+    __shared__ float xs_s[Q4K ? QT * DSTR : 1]; // Q4_K: d * sum(q) of each block, for the mins
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, kq = lane >> 4;
     const int G = N_XCD * a.n_rt, bid = blockIdx.x;
@@ -496,32 +584,18 @@ __global__ __launch_bounds__(QNTH) void k_q8_gu_exact(MvArgs a)
         beg = sl.beg;
         cnt = sl.cnt;
     }
-    DevMat M = shared ? a.sa : a.a;
+    const DevMat &M = shared ? a.sa : a.a;
     const DevMat &B = shared ? a.sb : a.b;
     const int rows = M.rows;
     // this lane's weight row: column n of the MFMA tile, gate rows then up
     const int orow = rt * (QW * 8) + wave * 8 + (n & 7);
-    const uint8_t *mq = n < 8 ? M.q : B.q, *ms = n < 8 ? M.s : B.s;
     const size_t wr = (size_t)e * rows + orow;
-    const uint4 *wq = reinterpret_cast<const uint4 *>(mq + wr * K) + 2 * kq;
-    const uint2 *wsc = reinterpret_cast<const uint2 *>(ms + wr * NB * 2);
-    // half-group h = (g, pi): units 2 kq, 2 kq + 1 of the row and the 4 f16
-    // scales of blocks 8 g + pi + 2 j
-    struct Half {
-        uint4 q[2];
-        uint2 s;
-    };
-    auto load = [&](int h, Half &w) {
-        const int g = h >> 1, pi = h & 1;
-        w.q[0] = wq[16 * g + 8 * pi];
-        w.q[1] = wq[16 * g + 8 * pi + 1];
-        w.s = wsc[(pi * (K / 64) + 4 * g) / 4];
-    };
-    Half w0, w1;
-    load(0, w0); // the first weights go out before the staging waits
+    const W wsrc(n < 8 ? M.q : B.q, n < 8 ? M.s : B.s, wr, kq);
+    typename W::Step w0, w1;
+    wsrc.load(0, w0); // the first weights go out before the staging waits
     // stage the slot's input rows: quants (chain layout, row stride XSTR
-    // units) and block scales [row][q8_scale order]; rows past the count
-    // repeat the last one (their results are not stored)
+    // units) and block scales (and Q4_K's block sums) [row][q8_scale order];
+    // rows past the count repeat the last one (their results are not stored)
     {
         constexpr int UPR = K / 16; // units per row
         for (int idx = tid; idx < QT * UPR; idx += QNTH) {
@@ -535,10 +609,10 @@ __global__ __launch_bounds__(QNTH) void k_q8_gu_exact(MvArgs a)
             const int ti = min(i, cnt - 1);
             const size_t ar = shared ? (size_t)(tok0 + ti) : (size_t)a.dp.pair_tok[beg + ti];
             xd_s[i * DSTR + bs] = a.xd[ar * NB + bs];
+            if (Q4K) xs_s[i * DSTR + bs] = a.xs[ar * NB + bs];
         }
     }
     __syncthreads();
-    const int npairs = (cnt + 1) / 2;
     // the A operand's mask: A row 8 tt + l keeps word l, which lane kq holds
     // as word 0 (l = 2 kq) or word 1 (l = 2 kq + 1) of its 8 bytes
     const int tt = (n >> 3), l = n & 7;
@@ -552,74 +626,290 @@ __global__ __launch_bounds__(QNTH) void k_q8_gu_exact(MvArgs a)
         for (int pi = 0; pi < 2; pi++)
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) acc[p][pi][jj] = 0.0f;
-    // pi a compile-time constant: it picks the chain accumulators
-    auto compute = [&](int g, auto pi_c, const Half &w) {
+    // the blocks 8 g + pi + 2 j, j = 0..3, of parity pi (a compile-time
+    // constant: it picks the chain accumulators)
+    auto compute = [&](int g, auto pi_c, const typename W::Step &w) {
         constexpr int pi = decltype(pi_c)::value;
-        // the weight row's 4 block scales as f32
         float dw[4];
+        long wo[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const uint32_t h2 = j < 2 ? w.s.x : w.s.y;
-            dw[j] = f16_to_f32((j & 1) ? h2 >> 16 : h2 & 0xFFFF);
+            dw[j] = W::scale(w, pi, j);
+            wo[j] = W::operand(w, pi, j);
         }
 #pragma unroll
         for (int p = 0; p < NPR; p++) {
             if (2 * p < cnt) { // uniform
-            // A: input row 2 p + tt's units 2 kq, 2 kq + 1 of the half-group
-            const uint4 *xr = xq_s + (2 * p + tt) * XSTR + 16 * g + 8 * pi + 2 * kq;
-            const uint4 x0 = xr[0], x1 = xr[1];
-            // d_x of the 4 blocks for this lane's D row (input row 2 p + drow)
-            const float4 dx = *reinterpret_cast<const float4 *>(xd_s + (2 * p + drow) * DSTR + pi * (K / 64) + 4 * g);
-            const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+                // A: input row 2 p + tt's units 2 kq, 2 kq + 1 of the parity
+                const uint4 *xr = xq_s + (2 * p + tt) * XSTR + 16 * g + 8 * pi + 2 * kq;
+                const uint4 x0 = xr[0], x1 = xr[1];
+                // d_x of the 4 blocks for this lane's D row (input row 2 p + drow)
+                const float4 dx = *reinterpret_cast<const float4 *>(xd_s + (2 * p + drow) * DSTR + pi * (K / 64) + 4 * g);
+                const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t lo = x0[j] & keep0, hi = x1[j] & keep1;
-                const long xo = (long)((uint64_t)lo | (uint64_t)hi << 32);
-                const long wo = (long)((uint64_t)w.q[0][j] | (uint64_t)w.q[1][j] << 32);
-                const i32x4 z = {0, 0, 0, 0};
-                const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo, wo, z, 0, 0, 0);
-                const float sb = dw[j] * dxs[j]; // f16(d_w) * d_x, as the reference
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t lo = x0[j] & keep0, hi = x1[j] & keep1;
+                    const long xo = (long)((uint64_t)lo | (uint64_t)hi << 32);
+                    const i32x4 z = {0, 0, 0, 0};
+                    const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo, wo[j], z, 0, 0, 0);
+                    const float sb = dw[j] * dxs[j]; // w_scale * d_x, as the reference
 #pragma unroll
-                for (int jj = 0; jj < 4; jj++) acc[p][pi][jj] = __builtin_fmaf((float)d[jj], sb, acc[p][pi][jj]);
-                if (DUMP) {
-                    // the block's int32: the sum of its 8 word dots
-                    int bs = d[0] + d[1] + d[2] + d[3];
-                    bs += __shfl_xor(bs, 16);
-                    int32_t *dump = n < 8 ? a.dump_a : a.dump_b;
-                    const int i = 2 * p + drow;
-                    if (dump && !(kq & 1) && i < cnt)
-                        dump[((size_t)(beg + i) * rows + orow) * NB + 8 * g + pi + 2 * j] = bs;
+                    for (int jj = 0; jj < 4; jj++) acc[p][pi][jj] = __builtin_fmaf((float)d[jj], sb, acc[p][pi][jj]);
+                    if (DUMP) {
+                        // the block's int32: the sum of its 8 word dots
+                        int bs = d[0] + d[1] + d[2] + d[3];
+                        bs += __shfl_xor(bs, 16);
+                        int32_t *dump = n < 8 ? a.dump_a : a.dump_b;
+                        const int i = 2 * p + drow;
+                        if (dump && !(kq & 1) && i < cnt)
+                            dump[((size_t)(beg + i) * rows + orow) * NB + 8 * g + pi + 2 * j] = bs;
+                    }
                 }
-            }
             }
             // one pair's LDS reads and MFMA results live at a time
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    // two half-groups per turn, loads one ahead
-    for (int h = 0; h < 2 * NG; h += 2) {
-        load(h + 1, w1);
-        compute(h >> 1, std::integral_constant<int, 0>(), w0);
-        if (h + 2 < 2 * NG) load(h + 2, w0);
-        compute(h >> 1, std::integral_constant<int, 1>(), w1);
+    auto step = [&](int h, const typename W::Step &w) {
+        if constexpr (W::BOTH) {
+            compute(h, std::integral_constant<int, 0>(), w);
+            compute(h, std::integral_constant<int, 1>(), w);
+        } else if (h & 1) {
+            compute(h >> 1, std::integral_constant<int, 1>(), w);
+        } else {
+            compute(h >> 1, std::integral_constant<int, 0>(), w);
+        }
+    };
+    // two steps per turn, loads one ahead
+    static_assert(W::STEPS % 2 == 0, "steps");
+    for (int h = 0; h < W::STEPS; h += 2) {
+        wsrc.load(h + 1, w1);
+        step(h, w0);
+        if (h + 2 < W::STEPS) wsrc.load(h + 2, w0);
+        step(h + 1, w1);
+    }
+    // Q4_K's mins, per (input row, weight row): the sum over super-blocks
+    // and sub-block pairs, in that order, of dmin * (m_a * s_a + m_b * s_b)
+    // (the chain kernels' q4k_mins), s the input row's block sums; super-
+    // blocks outermost so that each header is decoded once for all pairs
+    float mins[NPR];
+#pragma unroll
+    for (int p = 0; p < NPR; p++) mins[p] = 0.0f;
+    if constexpr (Q4K) {
+        const int4 *hd = reinterpret_cast<const int4 *>((n < 8 ? M.s : B.s) + wr * (K / 256) * 16);
+        for (int sbk = 0; sbk < K / 256; sbk++) {
+            const int4 h = hd[sbk];
+            const float dmin = f16_to_f32((uint32_t)h.x >> 16);
+            float mf[8];
+#pragma unroll
+            for (int sb = 0; sb < 8; sb++)
+                mf[sb] = (float)(sb < 4 ? byte_at4(h, 4 + sb + 4) & 63
+                                        : (byte_at4(h, 4 + sb + 4) >> 4) | ((byte_at4(h, 4 + sb) >> 6) << 4));
+#pragma unroll
+            for (int p = 0; p < NPR; p++) {
+                if (2 * p < cnt) {
+                    const float *sr = xs_s + (2 * p + drow) * DSTR;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int s2 = 4 * sbk + j;
+                        mins[p] = mins[p] + dmin * (mf[2 * j] * sr[lay::q8_scale(K, 2 * s2)] +
+                                                    mf[2 * j + 1] * sr[lay::q8_scale(K, 2 * s2 + 1)]);
+                    }
+                }
+            }
+        }
     }
     // the reference's tree: u_l = chain (0, l) + chain (1, l); v = u_l +
     // u_(l+4) (the lane with kq ^ 1 holds words 4..7); (v0 + v2) + (v1 + v3);
-    // then silu(gate) * up, up from column n + 8
+    // Q4_K then subtracts its mins; then silu(gate) * up, up from column n + 8
+    const bool store = n < 8 && !(kq & 1);
 #pragma unroll
     for (int p = 0; p < NPR; p++) {
-        if (2 * p >= cnt) break;
-        float v[4];
+        if (2 * p < cnt) {
+            float v[4];
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-            const float uu = acc[p][0][jj] + acc[p][1][jj];
-            v[jj] = uu + __shfl_xor(uu, 16);
+            for (int jj = 0; jj < 4; jj++) {
+                const float uu = acc[p][0][jj] + acc[p][1][jj];
+                v[jj] = uu + __shfl_xor(uu, 16);
+            }
+            float t = (v[0] + v[2]) + (v[1] + v[3]);
+            if constexpr (Q4K) t = t - mins[p];
+            const int i = 2 * p + drow;
+            const float up = __shfl_xor(t, 8);
+            if (store && i < cnt) a.out[(size_t)(beg + i) * rows + orow] = silu_mul_t(t, up, exp_tab);
         }
-        const float t = (v[0] + v[2]) + (v[1] + v[3]);
-        const float up = __shfl_xor(t, 8);
-        const int i = 2 * p + drow;
-        if (n < 8 && !(kq & 1) && i < cnt) a.out[(size_t)(beg + i) * rows + orow] = silu_mul_t(t, up, exp_tab);
     }
+}
+
+
+// ---------------------------------------------------------------------------
+// Q6_K down matrices at prefill sizes on the int8 matrix cores.
+//
+// biv's dot_q6k (quant.rs:651-686, x86 1475-1533) weighs each 16-element
+// half of a 32-element block by its own int8 sub-scale: isum = sc_0 *
+// dot16_0 + sc_1 * dot16_1 (exact int32), then d * d_x * isum.  Here
+// v_mfma_i32_16x16x32_i8 takes A = one block of 8 input rows, each twice:
+// A row 2 t + hh keeps only half hh of input row t (lanes kq = 2 hh, 2 hh + 1
+// hold that half's bytes); B = the block of 16 weight rows as q - 32.  D row
+// 2 t + hh, column n is dot16_hh of input row t and weight row n, exactly,
+// and lane (n, kq) holds both halves of input rows 2 kq and 2 kq + 1: isum
+// in integers, then the f32 scaling; the sum over blocks runs in an order of
+// its own (down's outputs only meet the combine).
+//
+// Weights (chain layout, layout.hpp): per 512 elements (four halves qq of a
+// row) the ql units 16 (qq / 4) + 8 pi + w hold ql word w of quarters pi and
+// pi + 2 of each half, the qh units 8 (qq / 4) + w qh word w; lane kq loads
+// words 2 kq and 2 kq + 1, i.e. bytes 8 kq .. 8 kq + 7 of every block.
+template <int K, bool DUMP>
+__global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
+{
+    constexpr int RT = QRT;
+    constexpr int NB = K / 32;
+    constexpr int NQ = K / 512;      // groups of four halves
+    constexpr int XSTR = K / 16 + 1; // staged quant row: 16-byte units (+1 against bank conflicts)
+    constexpr int DSTR = QT + 4;     // staged scales [block][pair], floats
+    static_assert(K % 512 == 0 && QT % 8 == 0, "shapes");
+    __shared__ uint4 xq_s[QT * XSTR];
+    __shared__ float xd_s[NB * DSTR];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, kq = lane >> 4;
+    const int G = N_XCD * a.n_rt, bid = blockIdx.x;
+    const int u = (bid / G) * N_XCD + bid % N_XCD, rt = (bid % G) / N_XCD;
+    if (u >= a.u_max + a.n_sh) return;
+    const bool shared = u < a.n_sh;
+    int e = 0, beg, cnt;
+    if (shared) {
+        const int tok0 = u * a.sh_chunk;
+        beg = a.P + tok0;
+        cnt = min(a.sh_chunk, a.T - tok0);
+    } else {
+        const Slot sl = a.dp.slots[u - a.n_sh];
+        if (sl.cnt == 0) return; // uniform over the workgroup
+        e = sl.expert;
+        beg = sl.beg;
+        cnt = sl.cnt;
+    }
+    const DevMat &M = shared ? a.sa : a.a;
+    const int rows = M.rows;
+    const int rw0 = rt * Q_ROWS_WG + wave * 16 * RT;
+    // stage the slot's input rows (as the Q8_0 down kernel)
+    {
+        constexpr int UPR = K / 16;
+        for (int idx = tid; idx < QT * UPR; idx += QNTH) {
+            const int i = idx / UPR, c = idx % UPR;
+            const size_t ar = beg + min(i, cnt - 1);
+            xq_s[i * XSTR + c] = reinterpret_cast<const uint4 *>(a.xq + ar * K)[c];
+        }
+        for (int idx = tid; idx < QT * NB; idx += QNTH) {
+            const int i = idx / NB, bs = idx % NB;
+            const size_t ar = beg + min(i, cnt - 1);
+            const int b = 2 * (bs % (K / 64)) + bs / (K / 64); // lay::q8_scale's inverse
+            xd_s[b * DSTR + i] = a.xd[ar * NB + bs];
+        }
+    }
+    __syncthreads();
+    // A's mask: row 2 t + hh keeps half hh, bytes 16 hh .. 16 hh + 15, which
+    // lanes kq = 2 hh and 2 hh + 1 hold
+    const uint32_t keep = ((n & 1) == (kq >> 1)) ? ~0u : 0u;
+    const int at = n >> 1; // A row's input row within the 8-row group
+    float acc[QT / 8][RT][2];
+#pragma unroll
+    for (int t = 0; t < QT / 8; t++)
+#pragma unroll
+        for (int r = 0; r < RT; r++) acc[t][r][0] = acc[t][r][1] = 0.0f;
+    for (int gq = 0; gq < NQ; gq++) {
+        // this lane's weight words of the group, per row tile
+        uint4 ql[RT][2][2], qh[RT][2];
+        int4 scv[RT][2];
+        float dsb[RT][2];
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const size_t row = (size_t)e * rows + rw0 + 16 * r + n;
+            const uint8_t *base = M.q + row * (K / 256) * 192;
+            const uint4 *pl = reinterpret_cast<const uint4 *>(base);
+            const uint4 *ph = reinterpret_cast<const uint4 *>(base + (K / 256) * 128);
+#pragma unroll
+            for (int pi = 0; pi < 2; pi++)
+#pragma unroll
+                for (int w = 0; w < 2; w++) ql[r][pi][w] = pl[16 * gq + 8 * pi + 2 * kq + w];
+#pragma unroll
+            for (int w = 0; w < 2; w++) qh[r][w] = ph[8 * gq + 2 * kq + w];
+            // sub-scales of the group's 16 blocks: [pi][hsel] runs of K / 64
+            const int8_t *sc = reinterpret_cast<const int8_t *>(M.s + row * (K / 16));
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                // scv[r][c]: bytes [pi = c][hsel = 0 / 1][s = 8 gq .. + 7] as two int2 halves
+                const uint2 s0 = *reinterpret_cast<const uint2 *>(sc + (2 * c + 0) * (K / 64) + 8 * gq);
+                const uint2 s1 = *reinterpret_cast<const uint2 *>(sc + (2 * c + 1) * (K / 64) + 8 * gq);
+                scv[r][c] = make_int4((int)s0.x, (int)s0.y, (int)s1.x, (int)s1.y);
+            }
+            const uint16_t *dp = reinterpret_cast<const uint16_t *>(M.d + row * (K / 256) * 2);
+            dsb[r][0] = f16_to_f32(dp[2 * gq]);
+            dsb[r][1] = f16_to_f32(dp[2 * gq + 1]);
+        }
+#pragma unroll
+        for (int bl = 0; bl < 16; bl++) { // block b = 16 gq + bl: half qq = 4 gq + bl / 4, quarter k = bl % 4
+            const int qq = bl >> 2, k = bl & 3, pi = k & 1, hi = k >> 1;
+            const int b = 16 * gq + bl;
+            const int s2 = 2 * (4 * gq + qq) + hi; // the sub-scale step of (pi, hsel)
+            // B: q - 32 of words 2 kq, 2 kq + 1 of block b, per row tile
+            long wo[RT];
+            int sc0[RT], sc1[RT];
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                uint32_t wv[2];
+#pragma unroll
+                for (int w = 0; w < 2; w++) {
+                    const uint32_t lo = (ql[r][pi][w][qq] >> (4 * hi)) & 0x0F0F0F0Fu;
+                    const uint32_t hb = ((qh[r][w][qq] >> (2 * k)) & 0x03030303u) << 4;
+                    wv[w] = (((lo | hb) | 0x80808080u) - 0x20202020u) ^ 0x80808080u; // bytewise q - 32
+                }
+                wo[r] = (long)((uint64_t)wv[0] | (uint64_t)wv[1] << 32);
+                const int sidx = s2 - 8 * gq; // 0..7 within the group's run
+                const int4 sv = scv[r][pi];
+                const uint32_t w0 = sidx < 4 ? (uint32_t)sv.x : (uint32_t)sv.y;
+                const uint32_t w1 = sidx < 4 ? (uint32_t)sv.z : (uint32_t)sv.w;
+                sc0[r] = (int)(int8_t)((w0 >> (8 * (sidx & 3))) & 0xFF);
+                sc1[r] = (int)(int8_t)((w1 >> (8 * (sidx & 3))) & 0xFF);
+            }
+            // the activations' block b: chain layout unit 16 g + 8 pi + w, word j
+            const int g = b >> 3, xpi = b & 1, j = (b >> 1) & 3;
+#pragma unroll
+            for (int t = 0; t < QT / 8; t++) {
+                if (8 * t >= cnt) break; // uniform
+                const uint4 *xr = xq_s + (8 * t + at) * XSTR + 16 * g + 8 * xpi + 2 * kq;
+                const uint32_t lo = xr[0][j] & keep, hi2 = xr[1][j] & keep;
+                const long xo = (long)((uint64_t)lo | (uint64_t)hi2 << 32);
+                const float2 dx = *reinterpret_cast<const float2 *>(xd_s + b * DSTR + 8 * t + 2 * kq);
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    const i32x4 z = {0, 0, 0, 0};
+                    const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo, wo[r], z, 0, 0, 0);
+                    const int is0 = sc0[r] * d[0] + sc1[r] * d[1], is1 = sc0[r] * d[2] + sc1[r] * d[3];
+                    const float dd = dsb[r][qq >> 1];
+                    acc[t][r][0] = __builtin_fmaf((float)is0, dd * dx.x, acc[t][r][0]);
+                    acc[t][r][1] = __builtin_fmaf((float)is1, dd * dx.y, acc[t][r][1]);
+                    if (DUMP && a.dump_a) { // the block int32s, for the taps
+                        const int i0 = 8 * t + 2 * kq, row = rw0 + 16 * r + n;
+                        if (i0 < cnt) a.dump_a[((size_t)(beg + i0) * rows + row) * NB + b] = is0;
+                        if (i0 + 1 < cnt) a.dump_a[((size_t)(beg + i0 + 1) * rows + row) * NB + b] = is1;
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // input rows 8 t + 2 kq + c, row rw0 + 16 r + n
+#pragma unroll
+    for (int t = 0; t < QT / 8; t++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int i = 8 * t + 2 * kq + c;
+            if (i < cnt) {
+#pragma unroll
+                for (int r = 0; r < RT; r++) a.out[(size_t)(beg + i) * rows + rw0 + 16 * r + n] = acc[t][r][c];
+            }
+        }
 }
 
 } // namespace
@@ -690,24 +980,41 @@ hipError_t launch_q8_down_t(MvArgs a, int routed, int shared, hipStream_t st)
             k_q8_down_mfma<KK, false><<<grid, QNTH, 0, st>>>(a);                                                \
         return hipGetLastError();                                                                               \
     }
-    BIV_Q8_CASE(2048)
-    BIV_Q8_CASE(1024)
-    BIV_Q8_CASE(512)
+    if (M.ty == T_Q8_0) {
+        BIV_Q8_CASE(2048)
+        BIV_Q8_CASE(1024)
+        BIV_Q8_CASE(512)
+    }
 #undef BIV_Q8_CASE
+#define BIV_Q6_CASE(KK)                                                                                         \
+    if (M.cols == KK) {                                                                                         \
+        if (a.dump_a)                                                                                           \
+            k_q6k_down_mfma<KK, true><<<grid, QNTH, 0, st>>>(a);                                                \
+        else                                                                                                    \
+            k_q6k_down_mfma<KK, false><<<grid, QNTH, 0, st>>>(a);                                               \
+        return hipGetLastError();                                                                               \
+    }
+    if (M.ty == T_Q6K) {
+        BIV_Q6_CASE(2048)
+        BIV_Q6_CASE(1024)
+        BIV_Q6_CASE(512)
+    }
+#undef BIV_Q6_CASE
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_q8_mfma_down(const MvArgs &a, hipStream_t st)
 {
     const bool has_shared = a.sa.q != nullptr;
-    if (has_shared && a.sa.cols == a.a.cols && a.sa.rows == a.a.rows) return launch_q8_down_t(a, 1, 1, st);
+    if (has_shared && a.sa.ty == a.a.ty && a.sa.cols == a.a.cols && a.sa.rows == a.a.rows)
+        return launch_q8_down_t(a, 1, 1, st);
     hipError_t err = launch_q8_down_t(a, 1, 0, st);
     if (err != hipSuccess || !has_shared) return err;
     return launch_q8_down_t(a, 0, 1, st);
 }
 
 
-hipError_t launch_q8_gu_t(MvArgs a, int routed, int shared, hipStream_t st)
+hipError_t launch_gu_t(MvArgs a, int routed, int shared, hipStream_t st)
 {
     const DevMat &M = routed ? a.a : a.sa;
     if (!routed) a.u_max = 0;
@@ -717,28 +1024,35 @@ hipError_t launch_q8_gu_t(MvArgs a, int routed, int shared, hipStream_t st)
     if (a.sh_chunk > QT || M.rows % (QW * 8)) return hipErrorInvalidValue;
     a.n_rt = M.rows / (QW * 8);
     const dim3 grid((unsigned)((slots + N_XCD - 1) / N_XCD * N_XCD * a.n_rt));
-#define BIV_Q8_CASE(KK)                                                                                         \
-    if (M.cols == KK) {                                                                                         \
-        if (a.dump_a || a.dump_b)                                                                               \
-            k_q8_gu_exact<KK, true><<<grid, QNTH, 0, st>>>(a);                                                  \
+    const bool dump = a.dump_a || a.dump_b;
+#define BIV_GU_CASE(TY, KK)                                                                                     \
+    if (M.ty == TY && M.cols == KK) {                                                                           \
+        if (dump)                                                                                               \
+            k_gu_exact<TY, KK, true><<<grid, QNTH, 0, st>>>(a);                                                 \
         else                                                                                                    \
-            k_q8_gu_exact<KK, false><<<grid, QNTH, 0, st>>>(a);                                                 \
+            k_gu_exact<TY, KK, false><<<grid, QNTH, 0, st>>>(a);                                                \
         return hipGetLastError();                                                                               \
     }
-    BIV_Q8_CASE(2048)
-    BIV_Q8_CASE(1024)
-    BIV_Q8_CASE(512)
-#undef BIV_Q8_CASE
+    BIV_GU_CASE(T_Q8_0, 2048)
+    BIV_GU_CASE(T_Q8_0, 1024)
+    BIV_GU_CASE(T_Q8_0, 512)
+    BIV_GU_CASE(T_Q4K, 2048)
+    BIV_GU_CASE(T_Q4K, 1024)
+    BIV_GU_CASE(T_Q4K, 512)
+#undef BIV_GU_CASE
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_q8_mfma_gateup(const MvArgs &a, hipStream_t st)
+hipError_t launch_mfma_gateup_exact(const MvArgs &a, hipStream_t st)
 {
+    // routed and shared in one launch when they share a type and shape
     const bool has_shared = a.sa.q != nullptr;
-    if (has_shared && a.sa.cols == a.a.cols && a.sa.rows == a.a.rows) return launch_q8_gu_t(a, 1, 1, st);
-    hipError_t err = launch_q8_gu_t(a, 1, 0, st);
+    if (a.a.ty != a.b.ty || (has_shared && a.sa.ty != a.sb.ty)) return hipErrorInvalidValue;
+    if (has_shared && a.sa.ty == a.a.ty && a.sa.cols == a.a.cols && a.sa.rows == a.a.rows)
+        return launch_gu_t(a, 1, 1, st);
+    hipError_t err = launch_gu_t(a, 1, 0, st);
     if (err != hipSuccess || !has_shared) return err;
-    return launch_q8_gu_t(a, 0, 1, st);
+    return launch_gu_t(a, 0, 1, st);
 }
 
 } // namespace biv

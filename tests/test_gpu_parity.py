@@ -264,6 +264,26 @@ def test_kquant_layer(orc, engine):
         full_parity(orc, engine, layer, moe, h)
 
 
+@pytest.mark.parametrize("T", [64, 100])
+def test_kquant_prefill(orc, engine, T):
+    """From T = 64 the K-quant experts run on the int8 matrix cores: Q4_K
+    gate/up bit for bit (word dots from masked MFMAs, the x86 chains and the
+    mins on the vector ALU), Q6_K down with exact block int32s (each 16-element
+    half times its sub-scale) summed in another order."""
+    print(f"case kquant prefill T={T}", flush=True)
+    layer, moe = layer_for(engine, seed=31, n_expert=32, types=(Q4K, Q4K, Q6K))
+    h = synth.make_tokens(400 + T, T, offsets=True)
+    full_parity(orc, engine, layer, moe, h, block_dots=T == 64, min_exact=0.0)
+
+
+def test_mixed_shared_types_prefill(orc, engine):
+    """Q4_K routed and Q8_0 shared gate/up at T = 70: two matrix-core launches."""
+    print("case mixed shared prefill", flush=True)
+    layer, moe = layer_for(engine, seed=41, n_expert=16, types=(Q4K, Q4K, Q6K), shared_types=(Q8_0, Q8_0, Q8_0))
+    h = synth.make_tokens(17, 70)
+    full_parity(orc, engine, layer, moe, h, block_dots=False, min_exact=0.0)
+
+
 def test_mixed_shared_types(orc, engine):
     """A shared expert in Q8_0 beside Q4_K/Q6_K experts runs in its own launch."""
     print("case mixed shared", flush=True)
