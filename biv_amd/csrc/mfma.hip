@@ -559,11 +559,17 @@ __global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
     using W = GuW<TY, K>;
     constexpr int NB = K / 32;
     constexpr int NPR = QT / 2;      // input-row pairs of a slot
-    constexpr int XSTR = K / 16 + 1; // staged quant row: 16-byte units (+1 against bank conflicts)
     constexpr int DSTR = NB + 4;     // staged scales [row][q8_scale order]: floats (16-byte aligned rows)
     constexpr bool Q4K = TY == T_Q4K;
     static_assert(QT % 2 == 0, "pairs of input rows");
-    __shared__ uint4 xq_s[QT * XSTR];
+    // The A operands, masked in advance: for input row i, block b and A row
+    // word l, the 8 bytes lane kq = l / 2 supplies ({word l, 0} for even l,
+    // {0, word l} for odd l), at ((i * NB + b) * 8 + l) * 8.  The lanes whose
+    // A row word is not theirs read zeros from a region past the operands,
+    // as long as every offset a step adds (< (NB + 8) * 64 bytes).
+    constexpr int XOPS = QT * NB * 8; // 8-byte operands
+    constexpr int XZERO = (NB + 8) * 8;
+    __shared__ uint2 xop_s[XOPS + XZERO];
     __shared__ float xd_s[QT * DSTR];
     __shared__ float xs_s[Q4K ? QT * DSTR : 1]; // Q4_K: d * sum(q) of each block, for the mins
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -593,17 +599,25 @@ __global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
     const W wsrc(n < 8 ? M.q : B.q, n < 8 ? M.s : B.s, wr, kq);
     typename W::Step w0, w1;
     wsrc.load(0, w0); // the first weights go out before the staging waits
-    // stage the slot's input rows: quants (chain layout, row stride XSTR
-    // units) and block scales (and Q4_K's block sums) [row][q8_scale order];
-    // rows past the count repeat the last one (their results are not stored)
+    // stage the slot's input rows: the masked A operands (from the chain
+    // layout: unit 16 g + 8 pi + l holds word l of blocks 8 g + pi + 2 j) and
+    // block scales (and Q4_K's block sums) [row][q8_scale order]; rows past
+    // the count repeat the last one (their results are not stored)
     {
         constexpr int UPR = K / 16; // units per row
         for (int idx = tid; idx < QT * UPR; idx += QNTH) {
             const int i = idx / UPR, c = idx % UPR;
             const int ti = min(i, cnt - 1);
             const size_t ar = shared ? (size_t)(tok0 + ti) : (size_t)a.dp.pair_tok[beg + ti];
-            xq_s[i * XSTR + c] = reinterpret_cast<const uint4 *>(a.xq + ar * K)[c];
+            const uint4 v = reinterpret_cast<const uint4 *>(a.xq + ar * K)[c];
+            const int g = c >> 4, pi = (c >> 3) & 1, l = c & 7;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int b = 8 * g + pi + 2 * j;
+                xop_s[(i * NB + b) * 8 + l] = (l & 1) ? make_uint2(0u, v[j]) : make_uint2(v[j], 0u);
+            }
         }
+        for (int idx = tid; idx < XZERO; idx += QNTH) xop_s[XOPS + idx] = make_uint2(0u, 0u);
         for (int idx = tid; idx < QT * NB; idx += QNTH) {
             const int i = idx / NB, bs = idx % NB;
             const int ti = min(i, cnt - 1);
@@ -613,10 +627,13 @@ __global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
         }
     }
     __syncthreads();
-    // the A operand's mask: A row 8 tt + l keeps word l, which lane kq holds
-    // as word 0 (l = 2 kq) or word 1 (l = 2 kq + 1) of its 8 bytes
+    // the A operand: A row 8 tt + l keeps word l of input row tt, which lane
+    // kq = l / 2 supplies; the other lanes read zeros (a base that does not
+    // move with the pair)
     const int tt = (n >> 3), l = n & 7;
-    const uint32_t keep0 = l == 2 * kq ? ~0u : 0u, keep1 = l == 2 * kq + 1 ? ~0u : 0u;
+    const bool mine = (l >> 1) == kq;
+    const uint2 *xbase = mine ? xop_s + tt * NB * 8 + l : xop_s + XOPS;
+    const int xpair = mine ? 2 * NB * 8 : 0; // operands from one pair to the next
     // this lane's D: input row kq / 2 of the pair, chains (pi, 4 (kq & 1) + jj)
     const int drow = kq >> 1;
     float acc[NPR][2][4];
@@ -640,16 +657,15 @@ __global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
 #pragma unroll
         for (int p = 0; p < NPR; p++) {
             if (2 * p < cnt) { // uniform
-                // A: input row 2 p + tt's units 2 kq, 2 kq + 1 of the parity
-                const uint4 *xr = xq_s + (2 * p + tt) * XSTR + 16 * g + 8 * pi + 2 * kq;
-                const uint4 x0 = xr[0], x1 = xr[1];
+                // A: input row 2 p + tt's masked operands of blocks 8 g + pi + 2 j
+                const uint2 *xr = xbase + p * xpair + (8 * g + pi) * 8;
                 // d_x of the 4 blocks for this lane's D row (input row 2 p + drow)
                 const float4 dx = *reinterpret_cast<const float4 *>(xd_s + (2 * p + drow) * DSTR + pi * (K / 64) + 4 * g);
                 const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const uint32_t lo = x0[j] & keep0, hi = x1[j] & keep1;
-                    const long xo = (long)((uint64_t)lo | (uint64_t)hi << 32);
+                    const uint2 xv = xr[16 * j];
+                    const long xo = (long)((uint64_t)xv.x | (uint64_t)xv.y << 32);
                     const i32x4 z = {0, 0, 0, 0};
                     const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo, wo[j], z, 0, 0, 0);
                     const float sb = dw[j] * dxs[j]; // w_scale * d_x, as the reference
