@@ -252,16 +252,27 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
 // the 32-chain order above, scale = 1 / sqrt(ss + eps), v *= scale * w.  A
 // 32-lane half wave per row; n a multiple of 32.
 // y may be x (in place).
+template <int NPL>
 __global__ __launch_bounds__(256) void k_rms_norm(const float *x, float *y, const float *__restrict__ w, int rows, int n,
                                                   float eps)
 {
+    // NPL > 0: n = 32 NPL, the row held in registers (all loads issued before
+    // the chain); NPL = 0: any n (a multiple of 32), read twice
     const int L = threadIdx.x & 31;
     const int row = blockIdx.x * (blockDim.x / 32) + (threadIdx.x >> 5);
     if (row >= rows) return; // uniform over the half wave; no shuffles cross halves
     const float *g = x + (size_t)row * n;
     float *o = y + (size_t)row * n;
     float acc = 0.0f;
-    for (int i = L; i < n; i += 32) acc = fmaf(g[i], g[i], acc);
+    float gv[NPL > 0 ? NPL : 1];
+    if constexpr (NPL > 0) {
+#pragma unroll
+        for (int k = 0; k < NPL; k++) gv[k] = g[L + 32 * k];
+#pragma unroll
+        for (int k = 0; k < NPL; k++) acc = fmaf(gv[k], gv[k], acc);
+    } else {
+        for (int i = L; i < n; i += 32) acc = fmaf(g[i], g[i], acc);
+    }
     float v = acc;
     v = v + __shfl_xor(v, 8);  // acc0+acc1 (lanes 0-7), acc2+acc3 (16-23)
     v = v + __shfl_xor(v, 16); // (acc0+acc1)+(acc2+acc3)
@@ -270,7 +281,12 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float *x, float *y, cons
     v = v + __shfl_xor(v, 1);  // movehdup
     const float ss = v / (float)n;
     const float scale = 1.0f / sqrtf(ss + eps);
-    for (int i = L; i < n; i += 32) o[i] = g[i] * (scale * w[i]);
+    if constexpr (NPL > 0) {
+#pragma unroll
+        for (int k = 0; k < NPL; k++) o[L + 32 * k] = gv[k] * (scale * w[L + 32 * k]);
+    } else {
+        for (int i = L; i < n; i += 32) o[i] = g[i] * (scale * w[i]);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1163,7 +1179,8 @@ hipError_t launch_mv(const MvArgs &a, hipStream_t st)
 hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, int n, float eps, hipStream_t st)
 {
     if (rows <= 0) return hipSuccess;
-    k_rms_norm<<<(rows + 7) / 8, 256, 0, st>>>(x, y, w, rows, n, eps);
+    if (n == 2048) k_rms_norm<64><<<(rows + 7) / 8, 256, 0, st>>>(x, y, w, rows, n, eps);
+    else k_rms_norm<0><<<(rows + 7) / 8, 256, 0, st>>>(x, y, w, rows, n, eps);
     return hipGetLastError();
 }
 
