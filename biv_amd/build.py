@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libbiv_hip.so")
-SOURCES = ["kernels.hip", "mfma.hip", "api.cpp"]
+SOURCES = ["kernels.hip", "mfma.hip", "api.cpp", "gguf.cpp"]
 ARCH = "gfx950"
 
 FLAGS = [

@@ -86,6 +86,13 @@ int fail(biv_hip_ctx *ctx, int code, const char *fmt, ...)
     return code;
 }
 
+} // namespace
+
+// the context's error from the GGUF loader (gguf.cpp)
+int biv_hip_fail_ext(biv_hip_ctx *ctx, int code, const char *msg) { return fail(ctx, code, "%s", msg); }
+
+namespace {
+
 int hip_fail(biv_hip_ctx *ctx, hipError_t e, const char *what)
 {
     return fail(ctx, BIV_HIP_E_DEVICE, "%s: %s", what, hipGetErrorString(e));

@@ -30,7 +30,9 @@ SYMBOLS = [
     "biv_hip_moe_forward_device", "biv_hip_moe_forward_taps", "biv_hip_malloc", "biv_hip_free",
     "biv_hip_memcpy_h2d", "biv_hip_memcpy_d2h", "biv_hip_numerics", "biv_hip_device_bytes",
     "biv_hip_set_timing", "biv_hip_stage_times", "biv_hip_time_stage", "biv_hip_rms_norm",
-    "biv_hip_moe_ffn_step",
+    "biv_hip_moe_ffn_step", "biv_hip_moe_from_gguf",
+    "biv_gguf_open", "biv_gguf_close", "biv_gguf_last_error", "biv_gguf_get_u64", "biv_gguf_get_f32",
+    "biv_gguf_get_str", "biv_gguf_n_tensors", "biv_gguf_tensor_name", "biv_gguf_tensor", "biv_gguf_read_moe_config",
 ]
 
 STAGES = ["router", "route_sort", "gate_up", "quant_act", "down", "combine"]

@@ -47,6 +47,9 @@ enum {
     BIV_HIP_E_TYPE = -2,    /* no kernel for this type (Error::NoKernel, model.rs:341-346) */
     BIV_HIP_E_DEVICE = -3,  /* HIP runtime failure */
     BIV_HIP_E_NOMEM = -4,   /* device allocation failed (Error::OutOfMemory) */
+    BIV_HIP_E_FORMAT = -5,  /* malformed GGUF (Error::Truncated, BadMagic, UnsupportedVersion, ...; error.rs:13-25) */
+    BIV_HIP_E_IO = -6,      /* a GGUF file cannot be opened or mapped */
+    BIV_HIP_E_MISSING = -7, /* GGUF key or tensor absent (Error::MissingKey / MissingTensor, error.rs:28-29) */
 };
 
 /* forward flags */
@@ -190,6 +193,56 @@ int biv_hip_moe_ffn_step(biv_hip_ctx *ctx, const biv_hip_moe *moe, float *x_dev,
  * whole passes only (src/bench.rs:86-103). */
 int biv_hip_time_stage(biv_hip_ctx *ctx, const biv_hip_moe *const *moes, int n_moes, const float *h_dev, int n,
                        float *out_dev, int stage, int reps, double *ms_per_launch);
+
+/* ---- GGUF files (biv's reader: engine/src/gguf.rs, engine/src/model.rs:298-421) ----
+ *
+ * A GGUF (or the shards of a split one, in order) memory-mapped and parsed
+ * as Gguf::from_shards does (gguf.rs:236-306): key/values of every value
+ * type, the tensor table, data at general.alignment (32 by default); for a
+ * key in several shards the first holds.  The handle keeps the mappings
+ * until biv_gguf_close.  A handle is used by one thread at a time. */
+typedef struct biv_gguf biv_gguf;
+
+int biv_gguf_open(const char *const *paths, int n_paths, biv_gguf **out);
+void biv_gguf_close(biv_gguf *g);
+/* The handle's last error, or that of the last failed biv_gguf_open on this
+ * thread when g is NULL (Error's Display, error.rs:74-90). */
+const char *biv_gguf_last_error(const biv_gguf *g);
+
+/* Metadata values (Gguf::get with Value::as_u64 / as_f32 / as_str,
+ * gguf.rs:40-75, 322-330).  BIV_HIP_E_MISSING for an absent key. */
+int biv_gguf_get_u64(biv_gguf *g, const char *key, uint64_t *out);
+int biv_gguf_get_f32(biv_gguf *g, const char *key, float *out);
+int biv_gguf_get_str(biv_gguf *g, const char *key, char *buf, size_t len);
+
+/* The tensor table in file order (Gguf::tensor_order) and Gguf::tensor
+ * (gguf.rs:340-350): type, dims in ggml order (dims[0] contiguous; unused
+ * dims 1), the mapped bytes and their size. */
+int biv_gguf_n_tensors(const biv_gguf *g);
+const char *biv_gguf_tensor_name(const biv_gguf *g, int i);
+int biv_gguf_tensor(biv_gguf *g, const char *name, int *ggml_type, int *n_dims, uint64_t dims[4], const void **data,
+                    size_t *n_bytes);
+
+/* The MoE part of Config (model.rs:70-120) for general.architecture
+ * "qwen35moe": n_layer = block_count - nextn_predict_layers, n_embd,
+ * expert_count, expert_used_count (1..expert_count), expert and shared
+ * expert feed-forward lengths (the shared one 0 when absent), the RMSNorm
+ * epsilon. */
+typedef struct {
+    char arch[32];
+    int n_layer, n_embd, n_expert, n_expert_used, n_ff_exp, n_ff_shexp;
+    float eps;
+} biv_gguf_moe_config;
+int biv_gguf_read_moe_config(biv_gguf *g, biv_gguf_moe_config *cfg);
+
+/* Loader::ffn for MoE layer `layer` (model.rs:386-421): checks the shapes of
+ * blk.<layer>.ffn_gate_inp (router), ffn_gate_exps + ffn_up_exps or the
+ * fused ffn_gate_up_exps (gate rows then up rows per expert, model.rs:
+ * 389-399), ffn_down_exps and, when expert_shared_feed_forward_length > 0,
+ * ffn_{gate,up,down}_shexp and ffn_gate_inp_shexp (Error::TensorShape as
+ * BIV_HIP_E_INVALID), uploads them from the mapping and creates the layer
+ * with k = expert_used_count (as biv_hip_moe_create). */
+int biv_hip_moe_from_gguf(biv_hip_ctx *ctx, biv_gguf *g, int layer, biv_hip_moe **out);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ from conftest import ROOT
 def header_functions():
     text = open(os.path.join(ROOT, "include", "biv_hip.h")).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(biv_hip_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(biv_(?:hip|gguf)_\w+)\s*\(", text)))
 
 
 def test_header_matches_python_binding():

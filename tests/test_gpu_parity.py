@@ -338,3 +338,31 @@ def test_empty_and_errors(engine):
         engine._check(engine.L.biv_hip_moe_create(engine.h, engine.upload_weight(layer.router), x, x, x,
                                                   None, None, None, None, 8, ctypes.byref(o)))
     assert e.value.code == -2
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_gguf_layers(orc, engine, tmp_path, fused):
+    """MoE layers loaded from a GGUF file (Loader::ffn, model.rs:386-421): the
+    same bits as the oracle on the layers written into it, fused gate_up
+    stack included; a tensor of the wrong shape is Error::TensorShape."""
+    from biv_amd import gguf
+    from biv_amd.hip import HipError
+    print(f"case gguf fused={fused}", flush=True)
+    layers = [synth.make_layer(71, n_expert=16, fused_gate_up=fused), synth.make_layer(72, n_expert=16)]
+    p = str(tmp_path / "moe.gguf")
+    gguf.write_moe(p, layers)
+    with gguf.Gguf(p) as g:
+        assert g.moe_config().n_layer == 2
+        for i, layer in enumerate(layers):
+            moe = gguf.moe_from_gguf(engine, g, i)
+            h = synth.make_tokens(80 + i, 5, offsets=True)
+            check_output(orc.moe(layer, h), moe.ffn(h))
+        with pytest.raises(HipError) as e:
+            gguf.moe_from_gguf(engine, g, 2)
+        assert "layer 2 of 2" in str(e.value)
+    tensors = gguf.moe_layer_tensors(0, layers[1])
+    tensors = [(n, t, [d[0], d[1] // 2, d[2]] if "down_exps" in n else d, b) for n, t, d, b in tensors]
+    gguf.write(p, gguf.moe_kv(layers[1:]), tensors)
+    with gguf.Gguf(p) as g, pytest.raises(HipError) as e:
+        gguf.moe_from_gguf(engine, g, 0)
+    assert "ffn_down_exps.weight has dims [512, 1024, 16], expected [512, 2048, 16]" in str(e.value)
