@@ -33,14 +33,17 @@ def hipcc():
             return p
 
 
-def build(verbose=False):
-    objdir = os.path.join(HERE, "_build")
+def build(verbose=False, defines=(), out=OUT):
+    """Compiles every source and links `out`.  `defines` (NAME=VALUE) select
+    tuning variants of the kernels for measurement; the default build takes
+    none."""
+    objdir = os.path.join(HERE, "_build" if not defines else "_build_" + "_".join(defines).replace("=", ""))
     os.makedirs(objdir, exist_ok=True)
     objs = []
     for src in SOURCES:
         obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
         lang = ["-x", "hip"]
-        cmd = [hipcc()] + FLAGS + lang + ["-I", os.path.join(ROOT, "include"), "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [hipcc()] + FLAGS + ["-D" + d for d in defines] + lang + ["-I", os.path.join(ROOT, "include"), "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd))
         r = subprocess.run(cmd, capture_output=True, text=True)
@@ -51,12 +54,16 @@ def build(verbose=False):
         if err.strip() and verbose:
             print(err)
         objs.append(obj)
-    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", OUT] + objs
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", out] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    return OUT
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    # python -m biv_amd.build [-v] [-DNAME=VALUE ... -o PATH]: a variant build
+    args = sys.argv[1:]
+    defs = [a[2:] for a in args if a.startswith("-D")]
+    out = args[args.index("-o") + 1] if "-o" in args else OUT
+    print(build(verbose="-v" in args, defines=defs, out=out))

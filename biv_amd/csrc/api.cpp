@@ -6,6 +6,7 @@
 #include "layout.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -68,6 +69,8 @@ struct biv_hip_ctx {
     // stage timing (biv_hip_set_timing): one event before each stage and
     // one after the last, per forward, read back by biv_hip_stage_times
     bool timing = false;
+    // down and combine in one launch at decode sizes (BIV_HIP_FUSED_DC=0 turns it off)
+    bool fused_dc = true;
     std::vector<hipEvent_t> ev_pool;
     std::vector<std::vector<hipEvent_t>> ev_fwd;
 };
@@ -473,7 +476,14 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     const bool down_q8 = m->down->m.ty != biv::T_BF16 || (has_shared && m->sd->m.ty != biv::T_BF16);
     const bool fused_quant = T <= 16 && !down_f32 && m->down->m.ty != biv::T_Q4K &&
                              (!has_shared || (m->sd->m.ty != biv::T_Q4K && m->sd->m.ty != biv::T_BF16));
-    if (down_q8 && (!fused_quant || dm.act) && run(3))
+    // Decode sizes: down and combine in one launch (each expert's pairs in
+    // one slot; Q8_0 or Q6_K down matrices, the shared one of the same kind)
+    const int dty = m->down->m.ty;
+    const bool fused_dc = ctx->fused_dc && T <= 16 && T <= chunk && (dty == biv::T_Q8_0 || dty == biv::T_Q6K) &&
+                          m->down->m.rows % 8 == 0 &&
+                          (!has_shared || (m->sd->m.ty == dty && m->sd->m.cols == m->down->m.cols &&
+                                           m->sd->m.rows == m->down->m.rows));
+    if (down_q8 && (!(fused_quant || fused_dc) || dm.act) && run(3))
         HIP_TRY(ctx, biv::launch_quant_rows(s.act, rows_act * ff / 32, ff, s.aq, s.ad, s.as, st), "quantise act");
     MARK();
 
@@ -491,6 +501,26 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     d.T = T;
     d.P = P;
     d.u_max = u_max;
+    if (fused_dc) {
+        if (run(4)) {
+            biv::DownCombineArgs c{};
+            c.a = m->down->m;
+            if (has_shared) c.sa = m->sd->m;
+            c.xf = s.act;
+            c.dp = s.dp;
+            c.glogit = s.glogit;
+            c.out = out;
+            c.dump = dm.down;
+            c.T = T;
+            c.P = P;
+            c.k = k;
+            c.add = (flags & BIV_HIP_ADD) != 0;
+            HIP_TRY(ctx, biv::launch_down_combine(c, st), "expert down + combine");
+        }
+        MARK();
+        MARK();
+        return 0;
+    }
     if (run(4)) {
         if (mf_dn) {
             biv::MfArgs g{};
@@ -553,6 +583,8 @@ int biv_hip_create(int device, biv_hip_ctx **out)
         return fail(nullptr, BIV_HIP_E_DEVICE, "stream: %s", hipGetErrorString(e));
     }
     ctx->stream = ctx->own;
+    const char *fdc = getenv("BIV_HIP_FUSED_DC");
+    ctx->fused_dc = !(fdc && fdc[0] == '0');
     *out = ctx;
     return 0;
 }

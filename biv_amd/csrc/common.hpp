@@ -113,6 +113,23 @@ hipError_t launch_quant_rows(const float *x, int n_blocks, int K, int8_t *qs, fl
 hipError_t launch_combine(const float *y, const Dispatch &dp, const float *glogit, int has_shared, int T, int P, int k,
                           int E, float *out, int add, hipStream_t st);
 
+// Down and combine in one launch at decode sizes (each expert's pairs in one
+// slot, so T <= the slot size): out[t] (+)= the combine of t's experts' down
+// rows, the intermediate xf quantised in the kernel.  Down matrices Q8_0 or
+// Q6_K, the shared expert's of the routed type and shape.
+struct DownCombineArgs {
+    DevMat a, sa;
+    const float *xf;     // f32 intermediate [P + T][K]
+    Dispatch dp;
+    const float *glogit;
+    float *out;
+    int32_t *dump;       // optional block-dot taps, as the down matvec's
+    int T, P, k, add;
+};
+// LDS bytes it needs for R intermediate rows of K and u_max slot records
+size_t down_combine_lds(int R, int K, int u_max);
+hipError_t launch_down_combine(const DownCombineArgs &a, hipStream_t st);
+
 // BF16 experts at prefill sizes on the matrix cores (mfma.hip).  The input
 // rows are first split into bf16 hi / lo halves (launch_split_bf16); gate/up
 // writes the f32 SwiGLU intermediate, down the f32 y rows, as the chain

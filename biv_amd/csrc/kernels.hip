@@ -317,6 +317,52 @@ __device__ inline unsigned wave_max_u32(unsigned v)
     return max(max(r0, r1), max(r2, r3));
 }
 
+// Top-k selection keys (k <= TOPK_FAST): the TOPK_FAST largest of the
+// wavefront's RPER keys per lane, as a list sorted in descending order, the
+// same in every lane.  Equal keys stay separate entries.
+constexpr int TOPK_FAST = 8;
+
+__device__ inline void cas_desc(unsigned &a, unsigned &b)
+{
+    const unsigned hi = max(a, b), lo = min(a, b);
+    a = hi;
+    b = lo;
+}
+
+__device__ inline void topk_lists(const unsigned (&key)[MAX_EXPERTS_PER_LANE], unsigned (&lst)[TOPK_FAST])
+{
+    static_assert(MAX_EXPERTS_PER_LANE == 4 && TOPK_FAST == 8, "list shapes (and the four rows of route_token)");
+    unsigned a0 = key[0], a1 = key[1], a2 = key[2], a3 = key[3];
+    cas_desc(a0, a1);
+    cas_desc(a2, a3);
+    cas_desc(a0, a2);
+    cas_desc(a1, a3);
+    cas_desc(a1, a2);
+    lst[0] = a0;
+    lst[1] = a1;
+    lst[2] = a2;
+    lst[3] = a3;
+#pragma unroll
+    for (int i = 4; i < TOPK_FAST; i++) lst[i] = 0u;
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+        unsigned m[TOPK_FAST];
+#pragma unroll
+        for (int i = 0; i < TOPK_FAST; i++) m[i] = (unsigned)__shfl_xor((int)lst[TOPK_FAST - 1 - i], off);
+        // the top half of a bitonic merge of two descending lists, then the
+        // half-cleaners that sort that bitonic sequence
+#pragma unroll
+        for (int i = 0; i < TOPK_FAST; i++) m[i] = max(lst[i], m[i]);
+#pragma unroll
+        for (int d = TOPK_FAST / 2; d >= 1; d >>= 1)
+#pragma unroll
+            for (int i = 0; i < TOPK_FAST; i++)
+                if ((i & d) == 0) cas_desc(m[i], m[i + d]);
+#pragma unroll
+        for (int i = 0; i < TOPK_FAST; i++) lst[i] = m[i];
+    }
+}
+
 // route (model.rs:256-268) of token t by one wavefront: softmax over the
 // logits (ops.rs:192-201), the k highest probabilities with the lower expert
 // first among equals, weights p / max(sum of the k in rank order, 1/16384).
@@ -342,22 +388,28 @@ __device__ void route_token(const float *__restrict__ logits, int n_expert, int 
     for (int j = 0; j < RPER; j++) {
         const int i = lane + WAVE * j;
         v[j] = i < n_expert ? exp_f32(v[j] - mx) : 0.0f;
-        if (i < n_expert) es[i] = v[j];
+        es[i] = v[j]; // zeros past n_expert: adding +0 leaves the positive sum's bits alone
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     // the sum in index order, as the reference's loop adds it: one chain, the
-    // same in every lane
+    // same in every lane; reads issued 16 values ahead of the adds
     float sum = 0.0f;
     const float4 *e4 = reinterpret_cast<const float4 *>(es);
-    for (int i = 0; i < n_expert / 4; i++) {
-        const float4 q = e4[i];
-        sum = sum + q.x;
-        sum = sum + q.y;
-        sum = sum + q.z;
-        sum = sum + q.w;
+    constexpr int NQ = MAX_EXPERTS_PER_LANE * WAVE / 4;
+#pragma unroll
+    for (int i0 = 0; i0 < NQ; i0 += 4) {
+        float4 q[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) q[u] = e4[i0 + u];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            sum = sum + q[u].x;
+            sum = sum + q[u].y;
+            sum = sum + q[u].z;
+            sum = sum + q[u].w;
+        }
     }
-    for (int i = n_expert & ~3; i < n_expert; i++) sum = sum + es[i];
     const float inv = 1.0f / sum;
     // probabilities as keys: bits + 1 orders like the float (p >= 0), 0 once taken
     unsigned key[RPER];
@@ -365,40 +417,90 @@ __device__ void route_token(const float *__restrict__ logits, int n_expert, int 
     for (int j = 0; j < RPER; j++) key[j] = lane + WAVE * j < n_expert ? __float_as_uint(v[j] * inv) + 1u : 0u;
     float sel_p = 0.0f, s = 0.0f;
     int sel_i = 0;
-    for (int r = 0; r < k; r++) {
-        unsigned best = 0;
+    if (k <= TOPK_FAST) {
+        // The k largest keys as a sorted list in every lane: each lane sorts
+        // its own, then six butterfly levels merge a lane's list with its
+        // partner's, keeping the top TOPK_FAST (bitonic merge).  Then the
+        // expert of rank r: the keys equal to the r-th, in index order,
+        // skipping those equal keys already ranked (lower index first).
+        unsigned lst[TOPK_FAST];
+        topk_lists(key, lst);
+        // every lane holds the same list: scalar values from here on
+        unsigned prev = 0u;
+        int before = 0; // earlier ranks holding the current key
 #pragma unroll
-        for (int j = 0; j < RPER; j++) best = max(best, key[j]);
-        best = wave_max_u32(best);
-        // the lowest index holding it: first row j, lowest lane
-        int bi = -1;
+        for (int r = 0; r < TOPK_FAST; r++) {
+            if (r >= k) break;
+            const unsigned kr = (unsigned)__builtin_amdgcn_readfirstlane((int)lst[r]);
+            before = r > 0 && prev == kr ? before + 1 : 0;
+            prev = kr;
+            // the before-th lowest index holding kr, rows j in index order
+            unsigned long long m[RPER];
 #pragma unroll
-        for (int j = 0; j < RPER; j++) {
-            const unsigned long long m = __ballot(key[j] == best && best != 0);
-            if (bi < 0 && m) bi = WAVE * j + __ffsll((long long)m) - 1;
-        }
-        float bp;
-        if (bi < 0) {
-            // NaN probabilities (non-finite h) give no candidate: the lowest
-            // expert not yet chosen keeps the ids in range
-            bi = 0;
-#pragma unroll
-            for (int j = RPER - 1; j >= 0; j--) {
-                const unsigned long long m = __ballot(lane + WAVE * j < n_expert && key[j] != 0);
-                if (m) bi = WAVE * j + __ffsll((long long)m) - 1;
+            for (int j = 0; j < RPER; j++) m[j] = __ballot(key[j] == kr);
+            int bi = 0, need = before;
+            int row = 0;
+            unsigned long long mm = m[0];
+            if (need >= __popcll(mm)) {
+                need -= __popcll(mm);
+                row = 1;
+                mm = m[1];
+                if (need >= __popcll(mm)) {
+                    need -= __popcll(mm);
+                    row = 2;
+                    mm = m[2];
+                    if (need >= __popcll(mm)) {
+                        need -= __popcll(mm);
+                        row = 3;
+                        mm = m[3];
+                    }
+                }
             }
-            bp = 0.0f;
-        } else {
-            bp = __uint_as_float(best - 1u);
+            for (int q = 0; q < need; q++) mm &= mm - 1ull;
+            bi = WAVE * row + __ffsll((long long)mm) - 1;
+            const float bp = __uint_as_float(kr - 1u); // kr >= 1: k <= n_expert valid keys
+            if (r == lane) {
+                sel_p = bp;
+                sel_i = bi;
+            }
+            s += bp; // the sum in rank order, as the reference's iterator sum
         }
+    } else {
+        for (int r = 0; r < k; r++) {
+            unsigned best = 0;
 #pragma unroll
-        for (int j = 0; j < RPER; j++)
-            if (lane + WAVE * j == bi) key[j] = 0;
-        if (r == lane) {
-            sel_p = bp;
-            sel_i = bi;
+            for (int j = 0; j < RPER; j++) best = max(best, key[j]);
+            best = wave_max_u32(best);
+            // the lowest index holding it: first row j, lowest lane
+            int bi = -1;
+#pragma unroll
+            for (int j = 0; j < RPER; j++) {
+                const unsigned long long m = __ballot(key[j] == best && best != 0);
+                if (bi < 0 && m) bi = WAVE * j + __ffsll((long long)m) - 1;
+            }
+            float bp;
+            if (bi < 0) {
+                // NaN probabilities (non-finite h) give no candidate: the lowest
+                // expert not yet chosen keeps the ids in range
+                bi = 0;
+#pragma unroll
+                for (int j = RPER - 1; j >= 0; j--) {
+                    const unsigned long long m = __ballot(lane + WAVE * j < n_expert && key[j] != 0);
+                    if (m) bi = WAVE * j + __ffsll((long long)m) - 1;
+                }
+                bp = 0.0f;
+            } else {
+                bp = __uint_as_float(best - 1u);
+            }
+#pragma unroll
+            for (int j = 0; j < RPER; j++)
+                if (lane + WAVE * j == bi) key[j] = 0;
+            if (r == lane) {
+                sel_p = bp;
+                sel_i = bi;
+            }
+            s += bp; // the sum in rank order, as the reference's iterator sum
         }
-        s += bp; // the sum in rank order, as the reference's iterator sum
     }
     s = fmaxf(s, 1.0f / 16384.0f);
     if (lane < k) {
@@ -540,9 +642,10 @@ __device__ inline void wave_lds_sync()
 
 // The same dispatch as sort_pairs for P <= 4 * WAVE pairs, by one wavefront
 // and without workgroup barriers.  A pair's place among its expert's pairs is
-// the number of earlier pairs with that expert (a token names an expert at
-// most once, so pair order is token order).  cnt, first and sfirst are LDS
-// arrays of MAX_EXPERTS.
+// the number of earlier tokens with that expert (a token names an expert at
+// most once), read from a token bitmap per expert; so T <= 64.  cnt is an
+// LDS array of 2 * MAX_EXPERTS ints (the bitmap reuses it), first and
+// sfirst of MAX_EXPERTS.
 __device__ void sort_pairs_wave(const int *ids, const float *wts, int n_expert, int k, int T, int chunk,
                                 const Dispatch &dp, int *cnt, int *first, int *sfirst)
 {
@@ -590,10 +693,16 @@ __device__ void sort_pairs_wave(const int *ids, const float *wts, int n_expert, 
     }
     for (int u = n_used + lane; u < dp.slot_cap; u += WAVE) reinterpret_cast<int4 *>(&dp.slots[u])[0] = make_int4(0, 0, 0, 0);
     wave_lds_sync();
+    // a pair's place among its expert's pairs: the earlier tokens with that
+    // expert, from a token bitmap per expert (T <= 4 * WAVE / k <= 64 here)
+    unsigned long long *bm = reinterpret_cast<unsigned long long *>(cnt); // cnt is read out above
+    for (int e = lane; e < MAX_EXPERTS; e += WAVE) bm[e] = 0ull;
+    wave_lds_sync();
+    for (int i = lane; i < P; i += WAVE) atomicOr(&bm[ids[i]], 1ull << (i / k));
+    wave_lds_sync();
     for (int i = lane; i < P; i += WAVE) {
         const int e = ids[i], t = i / k;
-        int r = 0;
-        for (int j = 0; j < i; j++) r += ids[j] == e;
+        const int r = __popcll(bm[e] & ((1ull << t) - 1ull));
         const int p = first[e] + r;
         dp.pair_tok[p] = t;
         dp.pair_exp[p] = e;
@@ -619,14 +728,14 @@ __global__ __launch_bounds__(RS_THREADS) void k_route_sort(const float *__restri
     __shared__ float es[RS_WAVES][MAX_EXPERTS];
     __shared__ int lds_ids[RS_WAVES * 16];
     __shared__ float lds_wts[RS_WAVES * 16];
-    const int wave = threadIdx.x >> 6;
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const bool single = gridDim.x == 1;
-    for (int t = blockIdx.x * RS_WAVES + wave; t < T; t += gridDim.x * RS_WAVES)
+    for (int t = blockIdx.x * nw + wave; t < T; t += gridDim.x * nw)
         route_token(logits, n_expert, k, t, es[wave], dp.ids, dp.wts, single ? lds_ids : nullptr,
                     single ? lds_wts : nullptr);
     if (single) {
         // the routes from LDS, sorted by one wavefront
-        __shared__ int cnt[MAX_EXPERTS], first[MAX_EXPERTS], sfirst[MAX_EXPERTS];
+        __shared__ int cnt[2 * MAX_EXPERTS], first[MAX_EXPERTS], sfirst[MAX_EXPERTS]; // cnt: later a u64 bitmap
         __syncthreads();
         if (wave == 0) sort_pairs_wave(lds_ids, lds_wts, n_expert, k, T, chunk, dp, cnt, first, sfirst);
         return;
@@ -1102,6 +1211,158 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a)
     *po = a.add ? *po + o : o;
 }
 
+// ---------------------------------------------------------------------------
+// Down and combine in one launch, for decode sizes (every expert's pairs in
+// one slot).  A workgroup owns RB output rows and computes them for every
+// routed expert and the shared expert, so that it holds all of a token's y
+// values for those rows and can combine them itself, in the reference's
+// order (model.rs:884-896): o = 0, o = fma(w, y, o) over the token's
+// experts in ascending id, then o = fma(sigmoid(g), y_shared, o).
+//
+// The workgroup first quantises the whole SwiGLU intermediate into LDS
+// (Q8Act, as the standalone quantiser, R = P + T rows), then its 16-lane
+// groups walk the (slot, row) units of its rows, each with the 16 chains of
+// biv's x86 dot, D units of weight rows in flight per group.
+constexpr int DC_RB = 8;    // output rows per workgroup
+#ifndef BIV_DC_WAVES
+#define BIV_DC_WAVES 16
+#endif
+#ifndef BIV_DC_DEPTH
+#define BIV_DC_DEPTH 2
+#endif
+constexpr int DC_WAVES = BIV_DC_WAVES; // waves per workgroup
+// weight rows in flight per group (at K = 512; fewer for longer rows)
+template <int K> constexpr int dc_depth() { return K <= 512 ? BIV_DC_DEPTH : K <= 1024 ? (BIV_DC_DEPTH + 1) / 2 : 1; }
+
+struct DcArgs {
+    DevMat a, sa;        // routed down stack, the shared expert's down (sa.q == nullptr without one)
+    const float *xf;     // the f32 intermediate [P + T][K]
+    Dispatch dp;
+    const float *glogit; // [T]
+    float *out;          // [T][rows]
+    int32_t *dump;       // optional [P + T][rows][K/32] block int32 dots
+    int T, P, k, add;
+    int u_max;           // slot records the sort wrote (dp.slot_cap)
+};
+
+template <int TY, int K, bool DUMP>
+__global__ __launch_bounds__(DC_WAVES *WAVE) void k_down_combine(DcArgs a)
+{
+    constexpr int S = K / 64;
+    constexpr int ROW16 = K / 16 + K / 128; // 16-byte pieces of a staged Q8 row
+    constexpr int NG = DC_WAVES * 4;        // 16-lane groups
+    constexpr int NTH = DC_WAVES * WAVE;
+    extern __shared__ int4 dyn[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int grp = tid >> 4, ln = lane & 15, pi = ln >> 3, l = ln & 7;
+    const int T = a.T, P = a.P, k = a.k;
+    const bool has_shared = a.sa.q != nullptr;
+    const int R = has_shared ? P + T : P;
+    const int rows = a.a.rows;
+    const int row0 = blockIdx.x * DC_RB;
+    int4 *stage = dyn;                                                // [R][ROW16]
+    float *ylds = reinterpret_cast<float *>(dyn + (size_t)R * ROW16); // [R][DC_RB]
+    int4 *slots = reinterpret_cast<int4 *>(ylds + (size_t)R * DC_RB); // [u_max + 1] {expert, beg, cnt, -}
+    __shared__ int n_used;
+    // slot heads (records with cnt 0 follow the used ones), the shared
+    // expert as the last slot
+    if (tid == 0) n_used = a.u_max;
+    __syncthreads();
+    for (int i = tid; i < a.u_max; i += NTH) {
+        const int4 h = *reinterpret_cast<const int4 *>(&a.dp.slots[i]);
+        slots[i] = h;
+        if (h.z == 0) atomicMin(&n_used, i);
+    }
+    __syncthreads();
+    const int U = n_used;
+    if (has_shared && tid == 0) slots[U] = make_int4(-1, P, T, 0);
+    __syncthreads();
+    const int nsl = U + (has_shared ? 1 : 0);
+    const int nunits = nsl * DC_RB;
+    const int per = (nunits + NG - 1) / NG; // units per group, uniform
+    // the matrix and row of unit v (a valid row past the last unit)
+    auto unit_row = [&](int v, int &slot, int &r) {
+        const int vv = v < nunits ? v : 0;
+        slot = vv / DC_RB;
+        r = row0 + vv % DC_RB;
+    };
+    auto load_unit = [&](Chain<TY, K> &c, int v) {
+        int slot, r;
+        unit_row(v, slot, r);
+        const int4 h = slots[slot];
+        const bool sh = h.x < 0;
+        c.load(sh ? a.sa : a.a, (size_t)(sh ? 0 : h.x) * rows + r, pi, l);
+    };
+    // the first weight rows go out before the intermediate is staged
+    constexpr int DC_D = dc_depth<K>();
+    Chain<TY, K> wc[DC_D];
+#pragma unroll
+    for (int d = 0; d < DC_D; d++) load_unit(wc[d], grp + d * NG);
+    // the intermediate, quantised into LDS: one 32-element block per thread and turn
+    for (int b = tid; b < R * (K / 32); b += NTH) {
+        const int r = b / (K / 32), bb = b - r * (K / 32);
+        float v[32];
+        load32(a.xf + (size_t)r * K + 32 * bb, v);
+        quant_block_at(v, K, bb, reinterpret_cast<int *>(&stage[r * ROW16]),
+                       reinterpret_cast<float *>(&stage[r * ROW16 + K / 16]), nullptr);
+    }
+    __syncthreads();
+    for (int i0 = 0; i0 < per; i0 += DC_D) {
+#pragma unroll
+        for (int d = 0; d < DC_D; d++) {
+            const int v = grp + (i0 + d) * NG;
+            if (v < nunits) {
+                int slot, r;
+                unit_row(v, slot, r);
+                const int4 h = slots[slot];
+                for (int j = 0; j < h.z; j++) {
+                    const int orow = h.y + j;
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < S / 4; q++) {
+                        const int4 xv = stage[orow * ROW16 + q * 16 + pi * 8 + l];
+                        const float4 xd = *reinterpret_cast<const float4 *>(&stage[orow * ROW16 + K / 16 + pi * (S / 4) + q]);
+                        const int xw[4] = {xv.x, xv.y, xv.z, xv.w};
+                        const float xs[4] = {xd.x, xd.y, xd.z, xd.w};
+#pragma unroll
+                        for (int c = 0; c < 4; c++) {
+                            const int s = 4 * q + c;
+                            const int p = wc[d].partial(s, xw[c]);
+                            acc = fmaf((float)p, wc[d].wscale(s) * xs[c], acc);
+                            if (DUMP) {
+                                int bs = p;
+                                bs += __shfl_xor(bs, 1);
+                                bs += __shfl_xor(bs, 2);
+                                bs += __shfl_xor(bs, 4);
+                                if (l == 0) a.dump[((size_t)orow * rows + r) * (K / 32) + 2 * s + pi] = bs;
+                            }
+                        }
+                    }
+                    float t = acc + __shfl_xor(acc, 8); // acc0 + acc1, lane by lane
+                    t = t + __shfl_xor(t, 4);           // the two 128-bit halves
+                    t = t + __shfl_xor(t, 2);           // movehl
+                    t = t + __shfl_xor(t, 1);           // movehdup
+                    if (ln == 0) ylds[orow * DC_RB + (r - row0)] = t;
+                }
+            }
+            load_unit(wc[d], v + DC_D * NG);
+        }
+    }
+    __syncthreads();
+    // the combine of this workgroup's rows
+    for (int i = tid; i < T * DC_RB; i += NTH) {
+        const int t = i / DC_RB, r = i - t * DC_RB;
+        float o = 0.0f;
+        for (int j = 0; j < k; j++) {
+            const int p = a.dp.tok_pairs[(size_t)t * k + j];
+            o = fmaf(a.dp.pair_w[p], ylds[p * DC_RB + r], o);
+        }
+        if (has_shared) o = fmaf(sigmoid(a.glogit[t]), ylds[(P + t) * DC_RB + r], o);
+        float *po = a.out + (size_t)t * rows + row0 + r;
+        *po = a.add ? *po + o : o;
+    }
+}
+
 template <int TY, int KK, bool GATEUP, bool DUMP, bool QX>
 hipError_t launch_case(const MvArgs &a, int rows, int slots, hipStream_t st)
 {
@@ -1215,7 +1476,8 @@ hipError_t launch_route_sort(const float *logits, int n_expert, int k, int T, in
 {
     // a single workgroup routes and sorts in LDS while every token has its wavefront
     const int groups = T <= RS_WAVES ? 1 : (T + RS_WAVES - 1) / RS_WAVES;
-    k_route_sort<<<groups, RS_THREADS, 0, st>>>(logits, n_expert, k, T, chunk, dp, counter);
+    const int threads = groups == 1 ? WAVE * T : RS_THREADS; // a wavefront per token
+    k_route_sort<<<groups, threads, 0, st>>>(logits, n_expert, k, T, chunk, dp, counter);
     return hipGetLastError();
 }
 
@@ -1233,6 +1495,40 @@ hipError_t launch_combine(const float *y, const Dispatch &dp, const float *glogi
     dim3 grid((E + 255) / 256, T);
     k_combine<<<grid, 256, 0, st>>>(c);
     return hipGetLastError();
+}
+
+size_t down_combine_lds(int R, int K, int u_max)
+{
+    return (size_t)R * (K / 16 + K / 128) * 16 + (size_t)R * DC_RB * 4 + (size_t)(u_max + 1) * 16;
+}
+
+hipError_t launch_down_combine(const DownCombineArgs &x, hipStream_t st)
+{
+    DcArgs a{x.a, x.sa, x.xf, x.dp, x.glogit, x.out, x.dump, x.T, x.P, x.k, x.add, x.dp.slot_cap};
+    const int K = a.a.cols, rows = a.a.rows;
+    if (rows % DC_RB || (a.sa.q && (a.sa.ty != a.a.ty || a.sa.cols != K || a.sa.rows != rows)))
+        return hipErrorInvalidValue;
+    const int R = a.sa.q ? a.P + a.T : a.P;
+    const size_t lds = down_combine_lds(R, K, a.u_max);
+    const bool dump = a.dump != nullptr;
+#define BIV_DC_CASE(TY, KK)                                                                                     \
+    if (a.a.ty == TY && K == KK) {                                                                              \
+        auto fn = dump ? k_down_combine<TY, KK, true> : k_down_combine<TY, KK, false>;                          \
+        if (lds > 65536) {                                                                                      \
+            hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+            if (e != hipSuccess) return e;                                                                      \
+        }                                                                                                       \
+        fn<<<rows / DC_RB, DC_WAVES * WAVE, lds, st>>>(a);                                                      \
+        return hipGetLastError();                                                                               \
+    }
+    BIV_DC_CASE(T_Q8_0, 512)
+    BIV_DC_CASE(T_Q8_0, 1024)
+    BIV_DC_CASE(T_Q8_0, 2048)
+    BIV_DC_CASE(T_Q6K, 512)
+    BIV_DC_CASE(T_Q6K, 1024)
+    BIV_DC_CASE(T_Q6K, 2048)
+#undef BIV_DC_CASE
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gateup(const MvArgs &a, hipStream_t st) { return launch_mv<true>(a, st); }

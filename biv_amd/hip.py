@@ -19,7 +19,9 @@ import numpy as np
 from . import synth
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libbiv_hip.so")
+# BIV_HIP_LIB names another build of the library (a tuning variant from
+# python -m biv_amd.build -D... -o PATH)
+LIB_PATH = os.environ.get("BIV_HIP_LIB") or os.path.join(HERE, "libbiv_hip.so")
 
 ADD = 1
 
