@@ -198,6 +198,34 @@ def bench_bf16_stack(eng, T, n_layers, passes, torch):
             "hbm_GBps": round(layer_bytes / (ms * 1e-3) / 1e9, 1)}
 
 
+def bench_dense(eng, copies, steps, warmup, torch, n_embd=4096, n_ff=12288):
+    """The dense SwiGLU FFN of the qwen35 dense models (dense_ffn,
+    model.rs:1118-1126) at a 9B-sized shape, Q8_0, T = 1 and 5, over `copies`
+    copies in HBM: a widening beside the MoE block, not a BASELINE config."""
+    from biv_amd import synth
+    layer = synth.make_dense(9, n_embd=n_embd, n_ff=n_ff)
+    dens = [eng.dense(layer) for _ in range(copies)]
+    wbytes = 3 * n_ff * (n_embd // 32) * 34
+    res = {"n_embd": n_embd, "n_ff": n_ff, "type": "Q8_0", "layers_rotated": copies, "weight_bytes": wbytes}
+    for T in (1, 5):
+        h_dev = torch.from_numpy(synth.make_tokens(1200 + T, T, n_embd=n_embd)).cuda()
+        out_dev = torch.empty_like(h_dev)
+        for i in range(warmup):
+            dens[i % copies].forward_device(h_dev.data_ptr(), T, out_dev.data_ptr())
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for i in range(steps):
+            dens[i % copies].forward_device(h_dev.data_ptr(), T, out_dev.data_ptr())
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        B = wbytes + 2 * T * n_embd * 4
+        res[str(T)] = {"us_per_layer": round(ms * 1e3, 3), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                       "GBps": round(B / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(B / (ms * 1e-3) / HBM_PEAK, 4)}
+    return res
+
+
 def bench_cpu(layer, T, seconds):
     """The oracle (C restatement of biv's AVX2/AVX-VNNI CPU path) on the host cores."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -227,9 +255,9 @@ def main():
     ap.add_argument("--T", type=int, default=5, help="tokens per step of the headline workload")
     ap.add_argument("--sweep", default="1,40,512", help="other T values to report ('' for none)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 to skip)")
-    ap.add_argument("--configs", default="kquant,bf16",
+    ap.add_argument("--configs", default="kquant,bf16,dense",
                     help="other BASELINE configs to run: kquant (Q4_K/Q6_K at T=1, 2048), bf16 (the 40-layer BF16 "
-                         "stack at T=4096); '' for none")
+                         "stack at T=4096), dense (the qwen35 dense FFN, 4096 x 12288 Q8_0); '' for none")
     ap.add_argument("--bf16-layers", type=int, default=40)
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (a kernel of known traffic, to scale "
@@ -274,6 +302,9 @@ def main():
         extra["kquant_q4k_q6k"] = {str(T): bench_config(eng, kq, 4, T, 50 if T <= 64 else 10, 5, torch)
                                    for T in (1, 2048)}
         log(f"kquant: {extra['kquant_q4k_q6k']}")
+    if "dense" in todo:
+        extra["dense_ffn"] = bench_dense(eng, 8, 100, 10, torch)
+        log(f"dense: {extra['dense_ffn']}")
     if "bf16" in todo:
         extra["bf16_stack"] = bench_bf16_stack(eng, 4096, args.bf16_layers, 2, torch)
         log(f"bf16 stack: {extra['bf16_stack']}")

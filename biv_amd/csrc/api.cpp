@@ -24,6 +24,12 @@ struct biv_hip_experts {
     DevMat m;
 };
 
+// A dense SwiGLU FFN layer (Ffn::Dense, model.rs:239-246)
+struct biv_hip_dense {
+    const biv_hip_weight *gate, *up, *down;
+    int E, ff;
+};
+
 struct biv_hip_moe {
     const biv_hip_weight *router, *sg, *su, *sd, *gi;
     const biv_hip_experts *gate, *up, *down;
@@ -31,6 +37,15 @@ struct biv_hip_moe {
 };
 
 namespace {
+
+// Device buffers of a dense forward, grown to the largest shape seen.
+struct DenseScratch {
+    int cap_T = 0, E = 0, ff = 0;
+    std::vector<void *> bufs;
+    int8_t *xq = nullptr, *aq = nullptr;
+    float *xd = nullptr, *xs = nullptr, *act = nullptr, *ad = nullptr, *as = nullptr;
+    float *h_stage = nullptr, *o_stage = nullptr;
+};
 
 // Device buffers of one forward, grown to the largest T seen.
 struct Scratch {
@@ -64,6 +79,8 @@ struct biv_hip_ctx {
     std::vector<biv_hip_moe *> layers;
     size_t bytes = 0;
     Scratch sc;
+    DenseScratch dsc;
+    std::vector<biv_hip_dense *> denses;
     // scratch shape: the widest layer seen
     int sc_E = 0, sc_ff = 0, sc_ne = 0, sc_k = 0;
     // stage timing (biv_hip_set_timing): one event before each stage and
@@ -170,12 +187,11 @@ int upload_mat(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, con
         return fail(ctx, BIV_HIP_E_INVALID, "width %zu: F32/BF16 rows must be a multiple of 128", cols);
     const int K = (int)cols;
     std::vector<uint8_t> q(nr * qrow), s(nr * srow), d(nr * drow);
-    // the matrices of a stack repack on several host threads (disjoint rows)
-    auto repack = [&](size_t e0, size_t e1) {
-    for (size_t e = e0; e < e1; e++)
-        for (size_t r = 0; r < rows; r++) {
+    // rows i0 .. i1 - 1 of the n * rows (disjoint ranges on several host threads)
+    auto repack = [&](size_t i0, size_t i1) {
+        for (size_t i = i0; i < i1; i++) {
+            const size_t e = i / rows, r = i % rows;
             const uint8_t *src = src_row(e, r);
-            const size_t i = e * rows + r;
             uint8_t *qd = &q[i * qrow], *sd = srow ? &s[i * srow] : nullptr, *dd = drow ? &d[i * drow] : nullptr;
             switch (ty) {
             case BIV_GGML_Q8_0:
@@ -238,10 +254,10 @@ int upload_mat(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, con
         }
     };
     {
-        const size_t nt = std::min<size_t>(n, std::max(1u, std::min(16u, std::thread::hardware_concurrency())));
+        const size_t nt = std::min<size_t>((nr + 255) / 256, std::max(1u, std::min(16u, std::thread::hardware_concurrency())));
         std::vector<std::thread> pool;
-        for (size_t t = 1; t < nt; t++) pool.emplace_back(repack, n * t / nt, n * (t + 1) / nt);
-        repack(0, n / nt);
+        for (size_t t = 1; t < nt; t++) pool.emplace_back(repack, nr * t / nt, nr * (t + 1) / nt);
+        repack(0, nr / nt);
         for (auto &th : pool) th.join();
     }
     int rc;
@@ -258,14 +274,91 @@ int upload_mat(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, con
     return 0;
 }
 
-template <class T> int sc_alloc(biv_hip_ctx *ctx, size_t count, T **out)
+template <class T> int sc_alloc(biv_hip_ctx *ctx, size_t count, T **out, std::vector<void *> *bufs = nullptr)
 {
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, count * sizeof(T) + 16);
     if (e != hipSuccess)
         return fail(ctx, BIV_HIP_E_NOMEM, "scratch hipMalloc(%zu): %s", count * sizeof(T), hipGetErrorString(e));
-    ctx->sc.bufs.push_back(p);
+    (bufs ? bufs : &ctx->sc.bufs)->push_back(p);
     *out = static_cast<T *>(p);
+    return 0;
+}
+
+void dense_scratch_free(biv_hip_ctx *ctx)
+{
+    for (void *p : ctx->dsc.bufs) (void)hipFree(p);
+    ctx->dsc = DenseScratch{};
+}
+
+// Make the dense scratch fit T rows of a layer of E x ff.
+int dense_scratch_fit(biv_hip_ctx *ctx, const biv_hip_dense *d, int T)
+{
+    DenseScratch &s = ctx->dsc;
+    if (T <= s.cap_T && d->E <= s.E && d->ff <= s.ff) return 0;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "sync");
+    const int cap = std::max(T, std::max(s.cap_T, 8)), E = std::max(d->E, s.E), ff = std::max(d->ff, s.ff);
+    dense_scratch_free(ctx);
+    const size_t Tc = cap;
+    auto *b = &s.bufs;
+    int rc = 0;
+    rc = rc ? rc : sc_alloc(ctx, Tc * E, &s.xq, b);
+    rc = rc ? rc : sc_alloc(ctx, Tc * E / 32, &s.xd, b);
+    rc = rc ? rc : sc_alloc(ctx, Tc * E / 32, &s.xs, b);
+    rc = rc ? rc : sc_alloc(ctx, Tc * ff, &s.act, b);
+    rc = rc ? rc : sc_alloc(ctx, Tc * ff, &s.aq, b);
+    rc = rc ? rc : sc_alloc(ctx, Tc * ff / 32, &s.ad, b);
+    rc = rc ? rc : sc_alloc(ctx, Tc * ff / 32, &s.as, b);
+    rc = rc ? rc : sc_alloc(ctx, Tc * E, &s.h_stage, b);
+    rc = rc ? rc : sc_alloc(ctx, Tc * E, &s.o_stage, b);
+    if (rc) {
+        dense_scratch_free(ctx);
+        return rc;
+    }
+    s.cap_T = cap;
+    s.E = E;
+    s.ff = ff;
+    return 0;
+}
+
+// dense_ffn (model.rs:1118-1126) of T rows on the context's stream:
+// Input::q8 of h (for quantised gate/up), gate/up with the SwiGLU, Q8 of
+// the intermediate (for a quantised down), down into out or added to it.
+int dense_forward(biv_hip_ctx *ctx, const biv_hip_dense *d, const float *h, int T, float *out, unsigned flags)
+{
+    if (T == 0) return 0;
+    int rc = dense_scratch_fit(ctx, d, T);
+    if (rc) return rc;
+    DenseScratch &s = ctx->dsc;
+    hipStream_t st = ctx->stream;
+    const int E = d->E, ff = d->ff;
+    const DevMat &G = d->gate->m, &U = d->up->m, &D = d->down->m;
+    if (G.ty != biv::T_BF16)
+        HIP_TRY(ctx, biv::launch_quant_rows(h, T * E / 32, E, s.xq, s.xd, s.xs, st), "quantise h");
+    biv::LongArgs g{};
+    g.a = G;
+    g.b = U;
+    g.xq = s.xq;
+    g.xd = s.xd;
+    g.xs = s.xs;
+    g.xf = h;
+    g.out = s.act;
+    g.T = T;
+    g.K = E;
+    HIP_TRY(ctx, biv::launch_long_mv(g, 1, st), "dense gate/up");
+    if (D.ty != biv::T_BF16)
+        HIP_TRY(ctx, biv::launch_quant_rows(s.act, T * ff / 32, ff, s.aq, s.ad, s.as, st), "quantise act");
+    biv::LongArgs dn{};
+    dn.a = D;
+    dn.xq = s.aq;
+    dn.xd = s.ad;
+    dn.xs = s.as;
+    dn.xf = s.act;
+    dn.out = out;
+    dn.T = T;
+    dn.K = ff;
+    dn.add = (flags & BIV_HIP_ADD) != 0;
+    HIP_TRY(ctx, biv::launch_long_mv(dn, 0, st), "dense down");
     return 0;
 }
 
@@ -602,6 +695,8 @@ void biv_hip_destroy(biv_hip_ctx *ctx)
     for (auto *w : ctx->weights) delete w;
     for (auto *x : ctx->experts) delete x;
     for (auto *l : ctx->layers) delete l;
+    for (auto *l : ctx->denses) delete l;
+    dense_scratch_free(ctx);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
 }
@@ -935,6 +1030,66 @@ int biv_hip_time_stage(biv_hip_ctx *ctx, const biv_hip_moe *const *moes, int n_m
     ctx->timing = timing;
     if (!rc) *ms_per_launch = ms / reps;
     return rc;
+}
+
+} // extern "C"
+
+extern "C" {
+
+int biv_hip_dense_create(biv_hip_ctx *ctx, const biv_hip_weight *gate, const biv_hip_weight *up,
+                         const biv_hip_weight *down, biv_hip_dense **out)
+{
+    if (!ctx) return BIV_HIP_E_INVALID;
+    if (!out || !gate || !up || !down) return fail(ctx, BIV_HIP_E_INVALID, "null argument");
+    *out = nullptr;
+    const DevMat &G = gate->m, &U = up->m, &D = down->m;
+    const int E = G.cols, ff = G.rows;
+    if (U.cols != E || U.rows != ff || D.cols != ff || D.rows != E)
+        return fail(ctx, BIV_HIP_E_INVALID, "dense shapes: gate %dx%d, up %dx%d, down %dx%d", G.rows, G.cols, U.rows,
+                    U.cols, D.rows, D.cols);
+    auto ok = [](int t) { return t == biv::T_Q8_0 || t == biv::T_Q4K || t == biv::T_Q6K || t == biv::T_BF16; };
+    if (!ok(G.ty) || !ok(D.ty) || U.ty != G.ty)
+        return fail(ctx, BIV_HIP_E_TYPE,
+                    "dense types gate %d, up %d, down %d: gate and up of one type, each Q8_0, Q4_K, Q6_K or BF16", G.ty,
+                    U.ty, D.ty);
+    if (E % 512 || ff % 512) return fail(ctx, BIV_HIP_E_INVALID, "n_embd %d and n_ff %d must be multiples of 512", E, ff);
+    auto *d = new biv_hip_dense{gate, up, down, E, ff};
+    ctx->denses.push_back(d);
+    *out = d;
+    return 0;
+}
+
+int biv_hip_dense_forward_device(biv_hip_ctx *ctx, const biv_hip_dense *d, const float *h_dev, int n, float *out_dev,
+                                 unsigned flags)
+{
+    if (!ctx) return BIV_HIP_E_INVALID;
+    if (!d) return fail(ctx, BIV_HIP_E_INVALID, "null layer");
+    if (n < 0) return fail(ctx, BIV_HIP_E_INVALID, "n = %d", n);
+    if (n > 0 && (!h_dev || !out_dev)) return fail(ctx, BIV_HIP_E_INVALID, "null h or out");
+    HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    return dense_forward(ctx, d, h_dev, n, out_dev, flags);
+}
+
+int biv_hip_dense_forward(biv_hip_ctx *ctx, const biv_hip_dense *d, const float *h, int n, float *out, unsigned flags)
+{
+    if (!ctx) return BIV_HIP_E_INVALID;
+    if (!d) return fail(ctx, BIV_HIP_E_INVALID, "null layer");
+    if (n < 0) return fail(ctx, BIV_HIP_E_INVALID, "n = %d", n);
+    if (n == 0) return 0;
+    if (!h || !out) return fail(ctx, BIV_HIP_E_INVALID, "null h or out");
+    HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    int rc = dense_scratch_fit(ctx, d, n);
+    if (rc) return rc;
+    DenseScratch &s = ctx->dsc;
+    const size_t bytes = sizeof(float) * (size_t)n * d->E;
+    HIP_TRY(ctx, hipMemcpyAsync(s.h_stage, h, bytes, hipMemcpyHostToDevice, ctx->stream), "copy h");
+    if (flags & BIV_HIP_ADD)
+        HIP_TRY(ctx, hipMemcpyAsync(s.o_stage, out, bytes, hipMemcpyHostToDevice, ctx->stream), "copy x");
+    rc = dense_forward(ctx, d, s.h_stage, n, s.o_stage, flags);
+    if (rc) return rc;
+    HIP_TRY(ctx, hipMemcpyAsync(out, s.o_stage, bytes, hipMemcpyDeviceToHost, ctx->stream), "copy out");
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "forward");
+    return 0;
 }
 
 } // extern "C"

@@ -130,6 +130,20 @@ struct DownCombineArgs {
 size_t down_combine_lds(int R, int K, int u_max);
 hipError_t launch_down_combine(const DownCombineArgs &a, hipStream_t st);
 
+// Matvecs over rows of any length K (a multiple of 512), the dense FFN's:
+// gate/up writes out[t][r] = silu(gate_r . x_t) * (up_r . x_t); down writes
+// out[t][r] = down_r . x_t, or adds it (add).  Quantised matrices read the
+// Q8 rows xq / xd (/ xs for Q4_K's mins), BF16 the f32 rows xf.
+struct LongArgs {
+    DevMat a, b;         // gate and up (b), or down (a)
+    const int8_t *xq;    // [T][K] chain layout
+    const float *xd, *xs;
+    const float *xf;     // [T][K] f32
+    float *out;          // [T][rows]
+    int T, K, add;
+};
+hipError_t launch_long_mv(const LongArgs &a, int gateup, hipStream_t st);
+
 // BF16 experts at prefill sizes on the matrix cores (mfma.hip).  The input
 // rows are first split into bf16 hi / lo halves (launch_split_bf16); gate/up
 // writes the f32 SwiGLU intermediate, down the f32 y rows, as the chain

@@ -358,7 +358,65 @@ int biv_gguf_read_moe_config(biv_gguf *g, biv_gguf_moe_config *cfg)
     return 0;
 }
 
+int biv_gguf_read_dense_config(biv_gguf *g, biv_gguf_dense_config *cfg)
+{
+    if (!g || !cfg) return BIV_HIP_E_INVALID;
+    memset(cfg, 0, sizeof *cfg);
+    int rc = biv_gguf_get_str(g, "general.architecture", cfg->arch, sizeof cfg->arch);
+    if (rc) return rc;
+    const std::string arch = cfg->arch;
+    if (arch != "qwen35") return g->fail(BIV_HIP_E_TYPE, "unsupported architecture " + arch + ": the dense loader takes qwen35");
+    auto need = [&](const char *k, uint64_t &v) { return biv_gguf_get_u64(g, (arch + "." + k).c_str(), &v); };
+    uint64_t block_count, nextn = 0, n_embd, n_ff;
+    if ((rc = need("block_count", block_count)) || (rc = need("embedding_length", n_embd)) ||
+        (rc = need("feed_forward_length", n_ff)))
+        return rc;
+    (void)need("nextn_predict_layers", nextn);
+    g->err.clear();
+    if (nextn > block_count) return g->fail(BIV_HIP_E_INVALID, "nextn_predict_layers > block_count");
+    float eps = 0.0f;
+    if ((rc = biv_gguf_get_f32(g, (arch + ".attention.layer_norm_rms_epsilon").c_str(), &eps))) return rc;
+    cfg->n_layer = (int)(block_count - nextn);
+    cfg->n_embd = (int)n_embd;
+    cfg->n_ff = (int)n_ff;
+    cfg->eps = eps;
+    return 0;
+}
+
 } // extern "C"
+
+// Loader::ffn for a dense layer (engine/src/model.rs:381-386): gate and up
+// `[n_embd, n_ff]`, down `[n_ff, n_embd]`, shapes checked as Loader::weight.
+extern "C" int biv_hip_dense_from_gguf(biv_hip_ctx *ctx, biv_gguf *g, int layer, biv_hip_dense **out)
+{
+    if (!ctx || !g || !out) return BIV_HIP_E_INVALID;
+    biv_gguf_dense_config cfg;
+    int rc = biv_gguf_read_dense_config(g, &cfg);
+    if (rc) return biv_hip_fail_ext(ctx, rc, g->err.c_str());
+    if (layer < 0 || layer >= cfg.n_layer)
+        return biv_hip_fail_ext(ctx, BIV_HIP_E_INVALID, fmt("layer %d of %d", layer, cfg.n_layer).c_str());
+    const size_t e = cfg.n_embd, ff = cfg.n_ff;
+    const std::string blk = "blk." + std::to_string(layer) + ".";
+    const TensorInfo *t[3];
+    const char *names[3] = {"ffn_gate", "ffn_up", "ffn_down"};
+    const std::vector<uint64_t> want[3] = {{e, ff}, {e, ff}, {ff, e}};
+    biv_hip_weight *w[3];
+    for (int i = 0; i < 3; i++) {
+        const std::string name = blk + names[i] + ".weight";
+        t[i] = g->tensor(name);
+        if (!t[i]) return biv_hip_fail_ext(ctx, BIV_HIP_E_MISSING, ("missing tensor " + name).c_str());
+        if (t[i]->dims != want[i]) {
+            std::string d, wd;
+            for (auto v : t[i]->dims) d += (d.empty() ? "" : ", ") + std::to_string(v);
+            for (auto v : want[i]) wd += (wd.empty() ? "" : ", ") + std::to_string(v);
+            return biv_hip_fail_ext(ctx, BIV_HIP_E_INVALID,
+                                    ("tensor " + name + " has dims [" + d + "], expected [" + wd + "]").c_str());
+        }
+        const void *data = g->shards[t[i]->shard].p + t[i]->offset;
+        if ((rc = biv_hip_upload_weight(ctx, t[i]->ty, want[i][0], want[i][1], data, &w[i]))) return rc;
+    }
+    return biv_hip_dense_create(ctx, w[0], w[1], w[2], out);
+}
 
 // Loader::ffn for a MoE layer (engine/src/model.rs:386-421), uploading each
 // matrix: the router `[n_embd, n_expert]`, the experts `[cols, rows, n]` (or

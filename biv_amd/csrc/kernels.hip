@@ -759,9 +759,12 @@ template <int K> struct Chain<T_Q8_0, K> {
     static constexpr int S = K / 64;
     int w[S];
     int hw[S / 2]; // the f16 scales, two per register
-    __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l)
+    // chunk c (elements cK .. cK + K - 1) of a row of KF elements: the
+    // quants of a chunk are contiguous, its scales sit at step cS of each
+    // parity's run
+    __device__ inline void load_chunk(const DevMat &M, size_t mrow, int KF, int c, int pi, int l)
     {
-        const int4 *q = reinterpret_cast<const int4 *>(M.q + mrow * K);
+        const int4 *q = reinterpret_cast<const int4 *>(M.q + mrow * KF + (size_t)c * K);
 #pragma unroll
         for (int i = 0; i < S / 4; i++) {
             int4 v = q[i * 16 + pi * 8 + l];
@@ -770,8 +773,9 @@ template <int K> struct Chain<T_Q8_0, K> {
             w[4 * i + 2] = v.z;
             w[4 * i + 3] = v.w;
         }
-        ld_words(M.s + 2 * (mrow * (K / 32) + pi * S), hw);
+        ld_words(M.s + 2 * (mrow * (KF / 32) + pi * (KF / 64) + (size_t)c * S), hw);
     }
+    __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l) { load_chunk(M, mrow, K, 0, pi, l); }
     __device__ inline int partial(int s, int x) const { return dot4(w[s], x, 0); }
     __device__ inline float wscale(int s) const
     {
@@ -786,9 +790,10 @@ template <int K> struct Chain<T_Q4K, K> {
     static constexpr int S = K / 64;
     int w[S];
     float ws[S];
-    __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l)
+    __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l) { load_chunk(M, mrow, K, 0, pi, l); }
+    __device__ inline void load_chunk(const DevMat &M, size_t mrow, int KF, int c, int pi, int l)
     {
-        const int4 *q = reinterpret_cast<const int4 *>(M.q + mrow * (K / 2));
+        const int4 *q = reinterpret_cast<const int4 *>(M.q + mrow * (KF / 2) + (size_t)c * (K / 2));
         const int sh = 4 * pi;
 #pragma unroll
         for (int i = 0; i < S / 4; i++) {
@@ -798,7 +803,7 @@ template <int K> struct Chain<T_Q4K, K> {
             w[4 * i + 2] = (int)(((unsigned)v.z >> sh) & 0x0F0F0F0Fu);
             w[4 * i + 3] = (int)(((unsigned)v.w >> sh) & 0x0F0F0F0Fu);
         }
-        const int4 *hd = reinterpret_cast<const int4 *>(M.s + 16 * (mrow * (K / 256)));
+        const int4 *hd = reinterpret_cast<const int4 *>(M.s + 16 * (mrow * (KF / 256) + (size_t)c * (K / 256)));
 #pragma unroll
         for (int i = 0; i < S / 4; i++) {
             const int4 h = hd[i];
@@ -826,11 +831,12 @@ template <int K> struct Chain<T_Q6K, K> {
     int sc[S];
     float dd[S / 4];
     int pi_;
-    __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l)
+    __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l) { load_chunk(M, mrow, K, 0, pi, l); }
+    __device__ inline void load_chunk(const DevMat &M, size_t mrow, int KF, int c, int pi, int l)
     {
-        const uint8_t *base = M.q + mrow * (K / 256) * 192;
-        const int4 *pl = reinterpret_cast<const int4 *>(base);
-        const int4 *ph = reinterpret_cast<const int4 *>(base + (K / 256) * 128);
+        const uint8_t *base = M.q + mrow * (KF / 256) * 192;
+        const int4 *pl = reinterpret_cast<const int4 *>(base + (size_t)c * (K / 256) * 128);
+        const int4 *ph = reinterpret_cast<const int4 *>(base + (KF / 256) * 128 + (size_t)c * (K / 256) * 64);
 #pragma unroll
         for (int i = 0; i < S / 8; i++) {
             int4 v = pl[i * 16 + pi * 8 + l];
@@ -845,12 +851,12 @@ template <int K> struct Chain<T_Q6K, K> {
             qh[4 * i + 3] = u.w;
         }
         int sw[S / 4];
-        ld_words(M.s + mrow * (K / 16) + lay::q6k_sc(K, pi, l >= 4, 0), sw);
+        ld_words(M.s + mrow * (KF / 16) + lay::q6k_sc(KF, pi, l >= 4, c * S), sw);
 #pragma unroll
         for (int i = 0; i < S / 4; i++)
 #pragma unroll
             for (int c = 0; c < 4; c++) sc[4 * i + c] = (int)(signed char)(((unsigned)sw[i] >> (8 * c)) & 0xFF);
-        const unsigned short *dp = reinterpret_cast<const unsigned short *>(M.d + 2 * mrow * (K / 256));
+        const unsigned short *dp = reinterpret_cast<const unsigned short *>(M.d + 2 * (mrow * (KF / 256) + (size_t)c * (K / 256)));
 #pragma unroll
         for (int i = 0; i < S / 4; i++) dd[i] = __half2float(__ushort_as_half(dp[i]));
         pi_ = pi;
@@ -870,9 +876,10 @@ template <int K> struct Chain<T_Q6K, K> {
 template <int K> struct Chain<T_BF16, K> {
     static constexpr int S = K / 16;
     int w[S / 2];
-    __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l)
+    __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l) { load_chunk(M, mrow, K, 0, pi, l); }
+    __device__ inline void load_chunk(const DevMat &M, size_t mrow, int KF, int c, int pi, int l)
     {
-        const int4 *q = reinterpret_cast<const int4 *>(M.q + mrow * K * 2);
+        const int4 *q = reinterpret_cast<const int4 *>(M.q + (mrow * KF + (size_t)c * K) * 2);
 #pragma unroll
         for (int g = 0; g < S / 8; g++) {
             const int4 v = q[g * 16 + pi * 8 + l];
@@ -942,6 +949,161 @@ __device__ inline float q4k_mins(const DevMat &M, size_t mrow, const float *xs, 
         }
     }
     return mins;
+}
+
+// The Q4_K mins of chunk c of a row of KF (q4k_mins over that chunk's
+// sub-block pairs), added to `mins` in the reference's order.
+template <int K>
+__device__ inline float q4k_mins_chunk(const DevMat &M, size_t mrow, int KF, int c, const float *xs, size_t xrow,
+                                       float mins)
+{
+    constexpr int S = K / 64;
+    const int4 *hd = reinterpret_cast<const int4 *>(M.s + 16 * (mrow * (KF / 256) + (size_t)c * (K / 256)));
+    const float *sr = xs + xrow * (KF / 32);
+    for (int i = 0; i < S / 4; i++) {
+        const int4 h = hd[i];
+        const float dmin = __half2float(__ushort_as_half((unsigned short)((unsigned)h.x >> 16)));
+        for (int j = 0; j < 4; j++) {
+            const int sa = 2 * j, sb = 2 * j + 1;
+            const int ma = sa < 4 ? byte_at(h, 4 + sa + 4) & 63
+                                  : (byte_at(h, 4 + sa + 4) >> 4) | ((byte_at(h, 4 + sa) >> 6) << 4);
+            const int mb = sb < 4 ? byte_at(h, 4 + sb + 4) & 63
+                                  : (byte_at(h, 4 + sb + 4) >> 4) | ((byte_at(h, 4 + sb) >> 6) << 4);
+            const int sg = c * S + 4 * i + j; // sub-block pair of the whole row
+            mins = mins + dmin * ((float)ma * sr[lay::q8_scale(KF, 2 * sg)] + (float)mb * sr[lay::q8_scale(KF, 2 * sg + 1)]);
+        }
+    }
+    return mins;
+}
+
+// ---------------------------------------------------------------------------
+// Matvecs over rows of any length (a multiple of LK): dense_ffn's gate/up
+// and down (model.rs:1118-1126) for the qwen35 dense FFN, whose rows are
+// longer than the experts'.  The row streams through in chunks of LK
+// elements; the 16 chains of a (row, token) run on across chunks, so every
+// sum is the reference's x86 order over the whole row.  A workgroup takes
+// LXT tokens and a block of rows: 8 of gate and up (the SwiGLU formed in
+// registers) or 16 of down.  Chunk c + 1's weights (registers) and
+// activations (LDS) load while chunk c computes.
+constexpr int LK = 512;
+constexpr int LXT = 8;
+
+template <int TY, bool GATEUP>
+__global__ __launch_bounds__(256) void k_chain_mv_long(LongArgs a)
+{
+    constexpr int K = LK, S = K / 64, ROW16 = K / 16 + K / 128, NTH = 256;
+    constexpr bool BF = TY == T_BF16;
+    constexpr int PIECES = BF ? LXT * K / 4 : LXT * ROW16; // 16-byte pieces of one chunk's rows
+    constexpr int NPC = (PIECES + NTH - 1) / NTH;
+    __shared__ int4 stage[2][NPC * NTH];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = lane >> 4, ln = lane & 15, pi = ln >> 3, l = ln & 7;
+    constexpr int RPW = GATEUP ? 2 : 4;
+    const int row = (blockIdx.x * 4 + wave) * RPW + (GATEUP ? grp >> 1 : grp);
+    const int m = GATEUP ? (grp & 1) : 0;
+    DevMat M = a.a;
+    if (GATEUP && m) { // up as gate plus a uniform offset (one pointer per plane)
+        M.q += a.b.q - M.q;
+        M.s += a.b.s - M.s;
+        M.d += a.b.d - M.d;
+    }
+    const int rows = M.rows, KF = a.K, nc = KF / K;
+    const bool row_ok = row < rows;
+    const size_t mrow = row_ok ? row : 0;
+    const int t0 = blockIdx.y * LXT, nt = min(LXT, a.T - t0);
+    const int np = BF ? nt * (K / 4) : nt * ROW16;
+    auto issue = [&](int c) {
+        int4 *dst = &stage[c & 1][0];
+#pragma unroll
+        for (int q = 0; q < NPC; q++) {
+            if (q * NTH >= np) break; // uniform
+            const int idx0 = q * NTH + (int)threadIdx.x, idx = idx0 < np ? idx0 : np - 1;
+            const void *src;
+            if constexpr (BF) {
+                const int j = idx / (K / 4), r = idx - j * (K / 4);
+                src = a.xf + (size_t)(t0 + j) * KF + (size_t)c * K + 4 * r;
+            } else {
+                const int j = idx / ROW16, r = idx - j * ROW16;
+                const size_t x = (size_t)(t0 + j);
+                if (r < K / 16) {
+                    src = a.xq + x * KF + (size_t)c * K + 16 * r;
+                } else { // scale pieces: parity, then 4 of its scales
+                    const int r2 = r - K / 16, ppi = r2 / (S / 4), qq = r2 - ppi * (S / 4);
+                    src = a.xd + x * (KF / 32) + ppi * (KF / 64) + (size_t)c * S + 4 * qq;
+                }
+            }
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(dst + q * NTH + wave * WAVE),
+                                             16, 0, 0);
+        }
+    };
+    float acc[LXT], mins[LXT];
+#pragma unroll
+    for (int j = 0; j < LXT; j++) {
+        acc[j] = 0.0f;
+        mins[j] = 0.0f;
+    }
+    auto compute = [&](const Chain<TY, K> &w, int c) {
+        const int4 *st = &stage[c & 1][0];
+#pragma unroll
+        for (int j = 0; j < LXT; j++) {
+            if (j >= nt) break;
+            if constexpr (BF) {
+                const float *xr = reinterpret_cast<const float *>(st) + j * K;
+#pragma unroll
+                for (int s2 = 0; s2 < K / 16; s2++) acc[j] = fmaf(w.wval(s2), xr[16 * s2 + ln], acc[j]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < S / 4; q++) {
+                    const int4 xv = st[j * ROW16 + q * 16 + pi * 8 + l];
+                    const float4 xd = *reinterpret_cast<const float4 *>(&st[j * ROW16 + K / 16 + pi * (S / 4) + q]);
+                    const int xw[4] = {xv.x, xv.y, xv.z, xv.w};
+                    const float xs[4] = {xd.x, xd.y, xd.z, xd.w};
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int s2 = 4 * q + u;
+                        acc[j] = fmaf((float)w.partial(s2, xw[u]), w.wscale(s2) * xs[u], acc[j]);
+                    }
+                }
+                if (TY == T_Q4K && ln == 0) mins[j] = q4k_mins_chunk<K>(M, mrow, KF, c, a.xs, (size_t)(t0 + j), mins[j]);
+            }
+        }
+    };
+    Chain<TY, K> w0, w1;
+    issue(0);
+    w0.load_chunk(M, mrow, KF, 0, pi, l);
+    for (int c = 0; c < nc; c += 2) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (c + 1 < nc) {
+            issue(c + 1);
+            w1.load_chunk(M, mrow, KF, c + 1, pi, l);
+        }
+        compute(w0, c);
+        if (c + 1 >= nc) break;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (c + 2 < nc) {
+            issue(c + 2);
+            w0.load_chunk(M, mrow, KF, c + 2, pi, l);
+        }
+        compute(w1, c + 1);
+    }
+#pragma unroll
+    for (int j = 0; j < LXT; j++) {
+        if (j >= nt) break;
+        float t = acc[j] + __shfl_xor(acc[j], 8); // acc0 + acc1, lane by lane
+        t = t + __shfl_xor(t, 4);                 // the two 128-bit halves
+        t = t + __shfl_xor(t, 2);                 // movehl
+        t = t + __shfl_xor(t, 1);                 // movehdup
+        if (TY == T_Q4K) t = t - __shfl(mins[j], lane & ~15);
+        const size_t o = (size_t)(t0 + j) * rows + row;
+        if (GATEUP) {
+            const float up = __shfl_xor(t, 16);
+            if (m == 0 && ln == 0 && row_ok) a.out[o] = silu_mul(t, up);
+        } else if (ln == 0 && row_ok) {
+            a.out[o] = a.add ? a.out[o] + t : t;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1528,6 +1690,27 @@ hipError_t launch_down_combine(const DownCombineArgs &x, hipStream_t st)
     BIV_DC_CASE(T_Q6K, 1024)
     BIV_DC_CASE(T_Q6K, 2048)
 #undef BIV_DC_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_long_mv(const LongArgs &a, int gateup, hipStream_t st)
+{
+    if (a.T <= 0) return hipSuccess;
+    if (a.K % LK || a.a.cols != a.K || (gateup && (a.b.ty != a.a.ty || a.b.cols != a.K || a.b.rows != a.a.rows)))
+        return hipErrorInvalidValue;
+    const int per_wg = gateup ? 8 : 16;
+    dim3 grid((a.a.rows + per_wg - 1) / per_wg, (a.T + LXT - 1) / LXT);
+#define BIV_LONG_CASE(TY)                                                                                       \
+    if (a.a.ty == TY) {                                                                                         \
+        if (gateup) k_chain_mv_long<TY, true><<<grid, 256, 0, st>>>(a);                                        \
+        else k_chain_mv_long<TY, false><<<grid, 256, 0, st>>>(a);                                              \
+        return hipGetLastError();                                                                               \
+    }
+    BIV_LONG_CASE(T_Q8_0)
+    BIV_LONG_CASE(T_Q4K)
+    BIV_LONG_CASE(T_Q6K)
+    BIV_LONG_CASE(T_BF16)
+#undef BIV_LONG_CASE
     return hipErrorInvalidValue;
 }
 

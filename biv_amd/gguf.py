@@ -23,6 +23,7 @@ U8, I8, U16, I16, U32, I32, F32, BOOL, STRING, ARRAY, U64, I64, F64 = range(13)
 _FMT = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f", BOOL: "<?", U64: "<Q",
         I64: "<q", F64: "<d"}
 
+E_INVALID, E_TYPE = -1, -2
 E_FORMAT, E_IO, E_MISSING = -5, -6, -7
 
 
@@ -120,6 +121,33 @@ def write_moe(path, layers, eps=1e-6, alignment=32):
     write(path, moe_kv(layers, eps), tensors, alignment=alignment)
 
 
+def dense_layer_tensors(i, layer: "synth.DenseLayer"):
+    """The tensors of blk.<i>'s dense FFN as Loader::ffn reads them
+    (model.rs:381-386): gate and up [n_embd, n_ff], down [n_ff, n_embd]."""
+    p = f"blk.{i}."
+    return [(p + "ffn_" + name + ".weight", w.ty, [w.cols, w.rows], w.data)
+            for name, w in (("gate", layer.gate), ("up", layer.up), ("down", layer.down))]
+
+
+def dense_kv(layers, eps=1e-6, arch="qwen35"):
+    """The metadata Config reads for a dense model's FFN (model.rs:70-131)."""
+    l0 = layers[0]
+    a = arch + "."
+    return [("general.architecture", arch), (a + "block_count", len(layers)), (a + "embedding_length", l0.n_embd),
+            (a + "feed_forward_length", l0.n_ff), (a + "attention.layer_norm_rms_epsilon", float(eps))]
+
+
+def write_dense(path, layers, eps=1e-6, alignment=32):
+    """A GGUF holding the dense FFNs of `layers` as blk.0.., with their config."""
+    tensors = [t for i, layer in enumerate(layers) for t in dense_layer_tensors(i, layer)]
+    write(path, dense_kv(layers, eps), tensors, alignment=alignment)
+
+
+class DenseConfig(ctypes.Structure):
+    _fields_ = [("arch", ctypes.c_char * 32), ("n_layer", ctypes.c_int), ("n_embd", ctypes.c_int),
+                ("n_ff", ctypes.c_int), ("eps", ctypes.c_float)]
+
+
 class MoeConfig(ctypes.Structure):
     _fields_ = [("arch", ctypes.c_char * 32), ("n_layer", ctypes.c_int), ("n_embd", ctypes.c_int),
                 ("n_expert", ctypes.c_int), ("n_expert_used", ctypes.c_int), ("n_ff_exp", ctypes.c_int),
@@ -146,6 +174,8 @@ def _lib():
                                   ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(vp), ctypes.POINTER(sz)]
     L.biv_gguf_read_moe_config.argtypes = [vp, ctypes.POINTER(MoeConfig)]
     L.biv_hip_moe_from_gguf.argtypes = [vp, vp, i, ctypes.POINTER(vp)]
+    L.biv_gguf_read_dense_config.argtypes = [vp, ctypes.POINTER(DenseConfig)]
+    L.biv_hip_dense_from_gguf.argtypes = [vp, vp, i, ctypes.POINTER(vp)]
     L._gguf_typed = True
     return L
 
@@ -221,6 +251,12 @@ class Gguf:
         return cfg
 
 
+    def dense_config(self):
+        cfg = DenseConfig()
+        self._check(self.L.biv_gguf_read_dense_config(self.h, ctypes.byref(cfg)))
+        return cfg
+
+
 class _LayerShape:
     """The shape facts HipMoe keeps, from a GGUF's MoE config."""
 
@@ -236,3 +272,12 @@ def moe_from_gguf(engine: "hip.HipEngine", g: Gguf, layer: int) -> "hip.HipMoe":
     out = ctypes.c_void_p()
     engine._check(engine.L.biv_hip_moe_from_gguf(engine.h, g.h, layer, ctypes.byref(out)))
     return hip.HipMoe(engine, out, _LayerShape(g.moe_config()))
+
+
+def dense_from_gguf(engine: "hip.HipEngine", g: Gguf, layer: int) -> "hip.HipDense":
+    """Loader::ffn for dense layer `layer` of the file, uploaded to the engine's GPU."""
+    _lib()
+    cfg = g.dense_config()
+    out = ctypes.c_void_p()
+    engine._check(engine.L.biv_hip_dense_from_gguf(engine.h, g.h, layer, ctypes.byref(out)))
+    return hip.HipDense(engine, out, cfg.n_embd, cfg.n_ff)

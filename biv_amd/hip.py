@@ -32,7 +32,8 @@ SYMBOLS = [
     "biv_hip_moe_forward_device", "biv_hip_moe_forward_taps", "biv_hip_malloc", "biv_hip_free",
     "biv_hip_memcpy_h2d", "biv_hip_memcpy_d2h", "biv_hip_numerics", "biv_hip_device_bytes",
     "biv_hip_set_timing", "biv_hip_stage_times", "biv_hip_time_stage", "biv_hip_rms_norm",
-    "biv_hip_moe_ffn_step", "biv_hip_moe_from_gguf",
+    "biv_hip_moe_ffn_step", "biv_hip_moe_from_gguf", "biv_hip_dense_create", "biv_hip_dense_forward",
+    "biv_hip_dense_forward_device", "biv_hip_dense_from_gguf", "biv_gguf_read_dense_config",
     "biv_gguf_open", "biv_gguf_close", "biv_gguf_last_error", "biv_gguf_get_u64", "biv_gguf_get_f32",
     "biv_gguf_get_str", "biv_gguf_n_tensors", "biv_gguf_tensor_name", "biv_gguf_tensor", "biv_gguf_read_moe_config",
 ]
@@ -89,6 +90,9 @@ def load():
     L.biv_hip_stage_times.argtypes = [vp, ctypes.POINTER(ctypes.c_double), i, ctypes.POINTER(ctypes.c_int)]
     L.biv_hip_rms_norm.argtypes = [vp, vp, vp, i, i, ctypes.c_float]
     L.biv_hip_moe_ffn_step.argtypes = [vp, vp, vp, vp, ctypes.c_float, i]
+    L.biv_hip_dense_create.argtypes = [vp, vp, vp, vp, pp]
+    L.biv_hip_dense_forward.argtypes = [vp, vp, vp, i, vp, ctypes.c_uint]
+    L.biv_hip_dense_forward_device.argtypes = [vp, vp, vp, i, vp, ctypes.c_uint]
     L.biv_hip_time_stage.argtypes = [vp, ctypes.POINTER(ctypes.c_void_p), i, vp, i, vp, i, i,
                                      ctypes.POINTER(ctypes.c_double)]
     _lib = L
@@ -157,6 +161,31 @@ class HipMoe:
                                                               ctypes.c_void_p(out_dev), ADD if add else 0))
 
 
+class HipDense:
+    """A dense SwiGLU FFN layer on the device: the counterpart of
+    Ffn::Dense (model.rs:239-246)."""
+
+    def __init__(self, ctx, handle, n_embd, n_ff):
+        self.ctx = ctx
+        self.handle = handle
+        self.n_embd = n_embd
+        self.n_ff = n_ff
+
+    def ffn(self, h, out=None, add=False):
+        """dense_ffn (model.rs:1118-1126) of the rows of h: host arrays."""
+        h = np.ascontiguousarray(h, dtype=np.float32).reshape(-1, self.n_embd)
+        n = h.shape[0]
+        if out is None:
+            out = np.zeros((n, self.n_embd), np.float32)
+        self.ctx._check(self.ctx.L.biv_hip_dense_forward(self.ctx.h, self.handle, _ptr(h), n, _ptr(out),
+                                                         ADD if add else 0))
+        return out
+
+    def forward_device(self, h_dev, n, out_dev, add=False):
+        self.ctx._check(self.ctx.L.biv_hip_dense_forward_device(self.ctx.h, self.handle, ctypes.c_void_p(h_dev), n,
+                                                                ctypes.c_void_p(out_dev), ADD if add else 0))
+
+
 class HipEngine:
     """A context on one GPU: owns the uploads, the scratch and the stream."""
 
@@ -211,6 +240,13 @@ class HipEngine:
         out = ctypes.c_void_p()
         self._check(self.L.biv_hip_moe_create(self.h, router, gate, up, down, *sh, layer.k, ctypes.byref(out)))
         return HipMoe(self, out, layer)
+
+    def dense(self, layer: "synth.DenseLayer"):
+        """Upload a dense FFN layer (gate, up, down) and create it."""
+        g, u, d = (self.upload_weight(w) for w in (layer.gate, layer.up, layer.down))
+        h = ctypes.c_void_p()
+        self._check(self.L.biv_hip_dense_create(self.h, g, u, d, ctypes.byref(h)))
+        return HipDense(self, h, layer.n_embd, layer.n_ff)
 
     def set_stream(self, stream_ptr):
         self._check(self.L.biv_hip_set_stream(self.h, ctypes.c_void_p(stream_ptr)))

@@ -239,6 +239,25 @@ def make_layer(seed, n_embd=2048, n_expert=256, k=8, n_ff=512, n_ff_sh=512, type
     return MoeLayer(n_embd, n_expert, k, n_ff, n_ff_sh if shared else 0, router, gate, up, down, sh)
 
 
+@dataclass(frozen=True)
+class DenseLayer:
+    """Ffn::Dense of a qwen35 layer (model.rs:239-246)."""
+    n_embd: int
+    n_ff: int
+    gate: Weight
+    up: Weight
+    down: Weight
+
+
+def make_dense(seed, n_embd=2048, n_ff=3584, types=(Q8_0, Q8_0, Q8_0), std=0.02):
+    """A dense SwiGLU FFN with weights ~N(0, std) from `seed`, quantised to
+    types = (gate, up, down)."""
+    rng = np.random.default_rng(seed)
+    gty, uty, dty = types
+    return DenseLayer(n_embd, n_ff, make_weight(rng, gty, n_embd, n_ff, std), make_weight(rng, uty, n_embd, n_ff, std),
+                      make_weight(rng, dty, n_ff, n_embd, std))
+
+
 def make_tokens(seed, T, n_embd=2048, offsets=False):
     """Hidden states ~N(0, 1), [T x n_embd] f32; with offsets, each token also
     gets a seeded offset vector of its own so tokens route to distinct experts."""

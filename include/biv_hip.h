@@ -141,6 +141,29 @@ typedef struct biv_hip_taps {
 int biv_hip_moe_forward_taps(biv_hip_ctx *ctx, const biv_hip_moe *moe, const float *h, int n, float *out,
                              unsigned flags, const biv_hip_taps *taps);
 
+/* A dense SwiGLU FFN layer, the FFN of biv's `qwen35` (dense) models:
+ * Ffn::Dense { gate, up, down } (engine/src/model.rs:239-246), loaded by
+ * Loader::ffn (model.rs:377-386).  gate and up [n_ff x n_embd] of one type,
+ * down [n_embd x n_ff]; each Q8_0, Q4_K, Q6_K or BF16; n_embd and n_ff
+ * multiples of 512.  Uploaded with biv_hip_upload_weight; the layer keeps
+ * pointers to them. */
+typedef struct biv_hip_dense biv_hip_dense;
+int biv_hip_dense_create(biv_hip_ctx *ctx, const biv_hip_weight *gate, const biv_hip_weight *up,
+                         const biv_hip_weight *down, biv_hip_dense **out);
+
+/* dense_ffn (model.rs:1118-1126) over n rows of h [n x n_embd] f32:
+ * out = down(silu(gate h) * up h), or out += it with BIV_HIP_ADD (the
+ * residual add of Model::layer, model.rs:788-790).  Every dot product runs
+ * in the reference's x86 accumulation order over the whole row, so the
+ * result is Model::ffn's for a dense layer.  Host pointers; returns when out
+ * is written. */
+int biv_hip_dense_forward(biv_hip_ctx *ctx, const biv_hip_dense *d, const float *h, int n, float *out,
+                          unsigned flags);
+
+/* The same with device pointers, queued on the context's stream. */
+int biv_hip_dense_forward_device(biv_hip_ctx *ctx, const biv_hip_dense *d, const float *h_dev, int n, float *out_dev,
+                                 unsigned flags);
+
 /* Device memory helpers for callers without another allocator. */
 int biv_hip_malloc(biv_hip_ctx *ctx, size_t bytes, void **out);
 int biv_hip_free(biv_hip_ctx *ctx, void *p);
@@ -243,6 +266,22 @@ int biv_gguf_read_moe_config(biv_gguf *g, biv_gguf_moe_config *cfg);
  * BIV_HIP_E_INVALID), uploads them from the mapping and creates the layer
  * with k = expert_used_count (as biv_hip_moe_create). */
 int biv_hip_moe_from_gguf(biv_hip_ctx *ctx, biv_gguf *g, int layer, biv_hip_moe **out);
+
+/* The dense part of Config (model.rs:70-131) for general.architecture
+ * "qwen35": n_layer = block_count - nextn_predict_layers, n_embd
+ * (embedding_length), n_ff (feed_forward_length), the RMSNorm epsilon. */
+typedef struct {
+    char arch[32];
+    int n_layer, n_embd, n_ff;
+    float eps;
+} biv_gguf_dense_config;
+int biv_gguf_read_dense_config(biv_gguf *g, biv_gguf_dense_config *cfg);
+
+/* Loader::ffn for dense layer `layer` (model.rs:381-386): checks
+ * blk.<layer>.ffn_gate and ffn_up [n_embd, n_ff] and ffn_down [n_ff, n_embd]
+ * (Error::TensorShape as BIV_HIP_E_INVALID), uploads them from the mapping
+ * and creates the layer (as biv_hip_dense_create). */
+int biv_hip_dense_from_gguf(biv_hip_ctx *ctx, biv_gguf *g, int layer, biv_hip_dense **out);
 
 #ifdef __cplusplus
 }

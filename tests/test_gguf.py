@@ -149,3 +149,27 @@ def test_reader_errors(tmp_path):
     gguf.write(q, [], [("t", 16, [256], b"\0" * 66)])
     assert "unknown type 16" in str(_err(q))
     assert _err(str(tmp_path / "absent.gguf")).code == gguf.E_IO
+
+
+def test_dense_config(tmp_path):
+    """The dense Config of a qwen35 file (model.rs:70-131), and the MoE
+    reader refusing it (and the other way round)."""
+    layer = synth.make_dense(5, n_embd=512, n_ff=1024)
+    p = str(tmp_path / "d.gguf")
+    gguf.write_dense(p, [layer, layer], eps=1e-5)
+    with gguf.Gguf(p) as g:
+        cfg = g.dense_config()
+        assert (cfg.arch, cfg.n_layer, cfg.n_embd, cfg.n_ff) == (b"qwen35", 2, 512, 1024)
+        assert cfg.eps == np.float32(1e-5)
+        with pytest.raises(HipError) as e:
+            g.moe_config()
+        assert e.value.code == gguf.E_TYPE
+        gty, dims, data = g.tensor("blk.1.ffn_down.weight")
+        assert (gty, dims) == (layer.down.ty, [1024, 512])
+        assert np.array_equal(data, layer.down.data)
+    pm = str(tmp_path / "m.gguf")
+    gguf.write_moe(pm, [small_layer()])
+    with gguf.Gguf(pm) as g:
+        with pytest.raises(HipError) as e:
+            g.dense_config()
+        assert e.value.code == gguf.E_TYPE
