@@ -987,19 +987,137 @@ __device__ inline float q4k_mins_chunk(const DevMat &M, size_t mrow, int KF, int
 // activations (LDS) load while chunk c computes.
 constexpr int LK = 512;
 constexpr int LXT = 8;
+#ifndef BIV_LONG_FULL_LDS
+#define BIV_LONG_FULL_LDS (96 * 1024)
+#endif
+constexpr size_t LONG_FULL_LDS = BIV_LONG_FULL_LDS; // LDS bytes up to which a workgroup stages every chunk
 
-template <int TY, bool GATEUP>
-__global__ __launch_bounds__(256) void k_chain_mv_long(LongArgs a)
+// FULL: every chunk of the workgroup's activation rows is staged in LDS
+// (dynamic, nc buffers) before the loop, so the loop only streams weights,
+// LPD chunks ahead in a ring of registers whose waits the compiler places.
+#ifndef BIV_LONG_LPD
+#define BIV_LONG_LPD 4
+#endif
+constexpr int LPD = BIV_LONG_LPD;
+
+template <int TY, bool GATEUP, int XTT, int WV>
+__global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long_full(LongArgs a)
 {
-    constexpr int K = LK, S = K / 64, ROW16 = K / 16 + K / 128, NTH = 256;
+    constexpr int K = LK, S = K / 64, ROW16 = K / 16 + K / 128, NTH = WV * WAVE;
     constexpr bool BF = TY == T_BF16;
-    constexpr int PIECES = BF ? LXT * K / 4 : LXT * ROW16; // 16-byte pieces of one chunk's rows
+    constexpr int PIECES = BF ? XTT * K / 4 : XTT * ROW16; // 16-byte pieces of one chunk's rows (XTT rows)
+    extern __shared__ int4 dyn[];                          // [nc][PIECES]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = lane >> 4, ln = lane & 15, pi = ln >> 3, l = ln & 7;
+    constexpr int RPW = GATEUP ? 2 : 4;
+    const int row = (blockIdx.x * WV + wave) * RPW + (GATEUP ? grp >> 1 : grp);
+    const int m = GATEUP ? (grp & 1) : 0;
+    DevMat M = a.a;
+    if (GATEUP && m) {
+        M.q += a.b.q - M.q;
+        M.s += a.b.s - M.s;
+        M.d += a.b.d - M.d;
+    }
+    const int rows = M.rows, KF = a.K, nc = KF / K;
+    const bool row_ok = row < rows;
+    const size_t mrow = row_ok ? row : 0;
+    const int t0 = blockIdx.y * XTT, nt = min(XTT, a.T - t0);
+    // the first weight chunks go out before the activations
+    Chain<TY, K> w[LPD];
+#pragma unroll
+    for (int d = 0; d < LPD; d++) w[d].load_chunk(M, mrow, KF, d < nc ? d : 0, pi, l);
+    // every chunk of the nt rows: piece (c, j, r) at dyn[c * PIECES + j * (BF ? K / 4 : ROW16) + r]
+    const int rp = BF ? K / 4 : ROW16, np = nt * rp;
+    for (int i = threadIdx.x; i < nc * np; i += NTH) {
+        const int c = i / np, jr = i - c * np, j = jr / rp, r = jr - j * rp;
+        const void *src;
+        if constexpr (BF) {
+            src = a.xf + (size_t)(t0 + j) * KF + (size_t)c * K + 4 * r;
+        } else {
+            const size_t x = (size_t)(t0 + j);
+            if (r < K / 16) {
+                src = a.xq + x * KF + (size_t)c * K + 16 * r;
+            } else {
+                const int r2 = r - K / 16, ppi = r2 / (S / 4), qq = r2 - ppi * (S / 4);
+                src = a.xd + x * (KF / 32) + ppi * (KF / 64) + (size_t)c * S + 4 * qq;
+            }
+        }
+        const int4 v = *reinterpret_cast<const int4 *>(src);
+        dyn[c * PIECES + jr] = v;
+    }
+    __syncthreads();
+    float acc[XTT], mins[XTT];
+#pragma unroll
+    for (int j = 0; j < XTT; j++) {
+        acc[j] = 0.0f;
+        mins[j] = 0.0f;
+    }
+    auto compute = [&](const Chain<TY, K> &wc, int c) {
+        const int4 *st = dyn + c * PIECES;
+#pragma unroll
+        for (int j = 0; j < XTT; j++) {
+            if (j >= nt) break;
+            if constexpr (BF) {
+                const float *xr = reinterpret_cast<const float *>(st) + j * K;
+#pragma unroll
+                for (int s2 = 0; s2 < K / 16; s2++) acc[j] = fmaf(wc.wval(s2), xr[16 * s2 + ln], acc[j]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < S / 4; q++) {
+                    const int4 xv = st[j * ROW16 + q * 16 + pi * 8 + l];
+                    const float4 xd = *reinterpret_cast<const float4 *>(&st[j * ROW16 + K / 16 + pi * (S / 4) + q]);
+                    const int xw[4] = {xv.x, xv.y, xv.z, xv.w};
+                    const float xs[4] = {xd.x, xd.y, xd.z, xd.w};
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int s2 = 4 * q + u;
+                        acc[j] = fmaf((float)wc.partial(s2, xw[u]), wc.wscale(s2) * xs[u], acc[j]);
+                    }
+                }
+                if (TY == T_Q4K && ln == 0) mins[j] = q4k_mins_chunk<K>(M, mrow, KF, c, a.xs, (size_t)(t0 + j), mins[j]);
+            }
+        }
+    };
+    for (int c0 = 0; c0 < nc; c0 += LPD) {
+#pragma unroll
+        for (int d = 0; d < LPD; d++) {
+            const int c = c0 + d;
+            if (c < nc) {
+                compute(w[d], c);
+                if (c + LPD < nc) w[d].load_chunk(M, mrow, KF, c + LPD, pi, l);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < XTT; j++) {
+        if (j >= nt) break;
+        float t = acc[j] + __shfl_xor(acc[j], 8); // acc0 + acc1, lane by lane
+        t = t + __shfl_xor(t, 4);                 // the two 128-bit halves
+        t = t + __shfl_xor(t, 2);                 // movehl
+        t = t + __shfl_xor(t, 1);                 // movehdup
+        if (TY == T_Q4K) t = t - __shfl(mins[j], lane & ~15);
+        const size_t o = (size_t)(t0 + j) * rows + row;
+        if (GATEUP) {
+            const float up = __shfl_xor(t, 16);
+            if (m == 0 && ln == 0 && row_ok) a.out[o] = silu_mul(t, up);
+        } else if (ln == 0 && row_ok) {
+            a.out[o] = a.add ? a.out[o] + t : t;
+        }
+    }
+}
+
+template <int TY, bool GATEUP, int XTT, int WV>
+__global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long(LongArgs a)
+{
+    constexpr int K = LK, S = K / 64, ROW16 = K / 16 + K / 128, NTH = WV * WAVE;
+    constexpr bool BF = TY == T_BF16;
+    constexpr int PIECES = BF ? XTT * K / 4 : XTT * ROW16; // 16-byte pieces of one chunk's rows
     constexpr int NPC = (PIECES + NTH - 1) / NTH;
     __shared__ int4 stage[2][NPC * NTH];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane >> 4, ln = lane & 15, pi = ln >> 3, l = ln & 7;
     constexpr int RPW = GATEUP ? 2 : 4;
-    const int row = (blockIdx.x * 4 + wave) * RPW + (GATEUP ? grp >> 1 : grp);
+    const int row = (blockIdx.x * WV + wave) * RPW + (GATEUP ? grp >> 1 : grp);
     const int m = GATEUP ? (grp & 1) : 0;
     DevMat M = a.a;
     if (GATEUP && m) { // up as gate plus a uniform offset (one pointer per plane)
@@ -1010,7 +1128,7 @@ __global__ __launch_bounds__(256) void k_chain_mv_long(LongArgs a)
     const int rows = M.rows, KF = a.K, nc = KF / K;
     const bool row_ok = row < rows;
     const size_t mrow = row_ok ? row : 0;
-    const int t0 = blockIdx.y * LXT, nt = min(LXT, a.T - t0);
+    const int t0 = blockIdx.y * XTT, nt = min(XTT, a.T - t0);
     const int np = BF ? nt * (K / 4) : nt * ROW16;
     auto issue = [&](int c) {
         int4 *dst = &stage[c & 1][0];
@@ -1036,16 +1154,16 @@ __global__ __launch_bounds__(256) void k_chain_mv_long(LongArgs a)
                                              16, 0, 0);
         }
     };
-    float acc[LXT], mins[LXT];
+    float acc[XTT], mins[XTT];
 #pragma unroll
-    for (int j = 0; j < LXT; j++) {
+    for (int j = 0; j < XTT; j++) {
         acc[j] = 0.0f;
         mins[j] = 0.0f;
     }
     auto compute = [&](const Chain<TY, K> &w, int c) {
         const int4 *st = &stage[c & 1][0];
 #pragma unroll
-        for (int j = 0; j < LXT; j++) {
+        for (int j = 0; j < XTT; j++) {
             if (j >= nt) break;
             if constexpr (BF) {
                 const float *xr = reinterpret_cast<const float *>(st) + j * K;
@@ -1089,7 +1207,7 @@ __global__ __launch_bounds__(256) void k_chain_mv_long(LongArgs a)
         compute(w1, c + 1);
     }
 #pragma unroll
-    for (int j = 0; j < LXT; j++) {
+    for (int j = 0; j < XTT; j++) {
         if (j >= nt) break;
         float t = acc[j] + __shfl_xor(acc[j], 8); // acc0 + acc1, lane by lane
         t = t + __shfl_xor(t, 4);                 // the two 128-bit halves
@@ -1693,19 +1811,58 @@ hipError_t launch_down_combine(const DownCombineArgs &x, hipStream_t st)
     return hipErrorInvalidValue;
 }
 
+#ifndef BIV_LONG_WV_GU
+#define BIV_LONG_WV_GU 4
+#endif
+#ifndef BIV_LONG_WV_DN
+#define BIV_LONG_WV_DN 4
+#endif
+
+template <int TY, bool GATEUP, int XTT>
+hipError_t launch_long_t(const LongArgs &a, bool full, size_t full_lds, hipStream_t st)
+{
+    // waves per workgroup; rows per workgroup: 2 (gate/up) or 4 (down) per wave
+    constexpr int WV = GATEUP ? BIV_LONG_WV_GU : BIV_LONG_WV_DN;
+    constexpr int per_wg = WV * (GATEUP ? 2 : 4);
+    dim3 grid((a.a.rows + per_wg - 1) / per_wg, (a.T + XTT - 1) / XTT);
+    if (full) {
+        auto fn = k_chain_mv_long_full<TY, GATEUP, XTT, WV>;
+        if (full_lds > 65536) {
+            hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)full_lds);
+            if (e != hipSuccess) return e;
+        }
+        fn<<<grid, WV * WAVE, full_lds, st>>>(a);
+    } else {
+        k_chain_mv_long<TY, GATEUP, XTT, WV><<<grid, WV * WAVE, 0, st>>>(a);
+    }
+    return hipGetLastError();
+}
+
+template <int TY, bool GATEUP>
+hipError_t launch_long_x(const LongArgs &a, hipStream_t st)
+{
+    // tokens per workgroup: as few accumulators as the batch needs
+    const int xt = a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : LXT;
+    // every chunk of a workgroup's rows in LDS when that fits (the weights
+    // then stream LPD chunks ahead), else two chunks at a time
+    const size_t piece_row = TY == T_BF16 ? LK / 4 : LK / 16 + LK / 128;
+    const size_t full_lds = (size_t)(a.K / LK) * xt * piece_row * 16;
+    const bool full = full_lds <= LONG_FULL_LDS;
+    switch (xt) {
+    case 1: return launch_long_t<TY, GATEUP, 1>(a, full, full_lds, st);
+    case 2: return launch_long_t<TY, GATEUP, 2>(a, full, full_lds, st);
+    case 4: return launch_long_t<TY, GATEUP, 4>(a, full, full_lds, st);
+    default: return launch_long_t<TY, GATEUP, LXT>(a, full, full_lds, st);
+    }
+}
+
 hipError_t launch_long_mv(const LongArgs &a, int gateup, hipStream_t st)
 {
     if (a.T <= 0) return hipSuccess;
     if (a.K % LK || a.a.cols != a.K || (gateup && (a.b.ty != a.a.ty || a.b.cols != a.K || a.b.rows != a.a.rows)))
         return hipErrorInvalidValue;
-    const int per_wg = gateup ? 8 : 16;
-    dim3 grid((a.a.rows + per_wg - 1) / per_wg, (a.T + LXT - 1) / LXT);
 #define BIV_LONG_CASE(TY)                                                                                       \
-    if (a.a.ty == TY) {                                                                                         \
-        if (gateup) k_chain_mv_long<TY, true><<<grid, 256, 0, st>>>(a);                                        \
-        else k_chain_mv_long<TY, false><<<grid, 256, 0, st>>>(a);                                              \
-        return hipGetLastError();                                                                               \
-    }
+    if (a.a.ty == TY) return gateup ? launch_long_x<TY, true>(a, st) : launch_long_x<TY, false>(a, st);
     BIV_LONG_CASE(T_Q8_0)
     BIV_LONG_CASE(T_Q4K)
     BIV_LONG_CASE(T_Q6K)
