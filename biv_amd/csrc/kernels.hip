@@ -247,6 +247,117 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
     }
 }
 
+// The router at prefill sizes, register-blocked: each 32-lane half wave runs
+// chain L of dot_f32 for 8 rows x 8 tokens (64 accumulators), so a value read
+// from LDS feeds 8 FMAs rather than one.  A workgroup (8 half waves) takes 16
+// rows x 32 tokens.  Both operands go straight from global memory into LDS,
+// RT_KC steps of 32 elements at a time: the router
+// rows as stored (f32 chain layout: lane L's four steps in one 16-byte word),
+// the tokens row-major (lane L reads element 32 s + L, conflict-free), into
+// two buffers, one stage ahead of the compute.  Per (row, token) every FMA is the
+// reference's, in its order, then the same tree: the logits carry k_router's
+// bits.
+constexpr int RT_ROWS = 16, RT_TOKS = 32, RT_KC = 4; // RT_KC steps of 32 elements per stage
+constexpr int RT_MIN_T = 64;                          // tokens from which launch_router takes it
+
+__global__ __launch_bounds__(256) void k_router_tiled(RouterArgs a, int n_tr, int n_tt)
+{
+    const int E = a.E, ne = a.n_expert, T = a.T, tid = threadIdx.x;
+    const int tile = blockIdx.x;
+    if (tile >= n_tr * n_tt) {
+        // the Q8 of h for the experts, in the workgroups past the tiles
+        const int nq = gridDim.x - n_tr * n_tt;
+        for (int i = (tile - n_tr * n_tt) * 256 + tid; i < T * (E / 32); i += nq * 256) {
+            float v[32];
+            load32(a.h + 32 * (size_t)i, v);
+            quant_block(v, E, i / (E / 32), i % (E / 32), a.xq, a.xd, a.xs);
+        }
+        return;
+    }
+    // row tiles fastest, so that consecutive workgroups share a token tile
+    const int tr = tile % n_tr, tt = tile / n_tr;
+    const int r0 = tr * RT_ROWS, t0 = tt * RT_TOKS;
+    constexpr int WP = RT_KC / 4 * 32;       // 16-byte words of a router row's stage
+    constexpr int XP = RT_KC * 32 / 4;       // 16-byte words of a token's stage
+    constexpr int NW = RT_ROWS * WP / 256;   // words per thread
+    constexpr int NX = RT_TOKS * XP / 256;
+    static_assert(NW * 256 == RT_ROWS * WP && NX * 256 == RT_TOKS * XP, "whole waves of 16-byte words");
+    __shared__ float4 Wl[2][RT_ROWS * WP];
+    __shared__ float4 Xl[2][RT_TOKS * XP];
+    const int lane = tid & 31, hw = tid >> 5, rg = hw & 1, tg = hw >> 1, wv = tid >> 6;
+    auto lds = [](const void *src, float4 *dst_wave) {
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst_wave, 16, 0, 0);
+    };
+    auto issue = [&](int c) {
+        const int b = c & 1;
+#pragma unroll
+        for (int q = 0; q < NW; q++) {
+            const int i = q * 256 + tid, r = i / WP, f = i - r * WP, row = r0 + r;
+            const float *w = row < ne ? a.router + (size_t)row * E : (row == ne && a.gate_inp ? a.gate_inp : a.router);
+            lds(reinterpret_cast<const float4 *>(w) + (size_t)c * WP + f, &Wl[b][q * 256 + wv * WAVE]);
+        }
+#pragma unroll
+        for (int q = 0; q < NX; q++) {
+            const int i = q * 256 + tid, t = i / XP, f = i - t * XP, tok = min(t0 + t, T - 1);
+            lds(reinterpret_cast<const float4 *>(a.h + (size_t)tok * E + (size_t)c * RT_KC * 32) + f,
+                &Xl[b][q * 256 + wv * WAVE]);
+        }
+    };
+    float acc[8][8];
+#pragma unroll
+    for (int r = 0; r < 8; r++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) acc[r][t] = 0.0f;
+    const int nc = E / 32 / RT_KC;
+    // two buffers: chunk c + 1 loads while chunk c computes (three, two
+    // ahead, measured slower: 72 KB of LDS leaves two workgroups per CU)
+    issue(0);
+    for (int c = 0; c < nc; c++) {
+        __builtin_amdgcn_s_waitcnt(0); // this chunk's stage (the only loads in flight)
+        __syncthreads();
+        if (c + 1 < nc) issue(c + 1);
+        const int b = c & 1;
+        const float *xb = reinterpret_cast<const float *>(&Xl[b][0]);
+#pragma unroll
+        for (int s4 = 0; s4 < RT_KC / 4; s4++) {
+            float4 w[8];
+#pragma unroll
+            for (int r = 0; r < 8; r++) w[r] = Wl[b][(rg * 8 + r) * WP + s4 * 32 + lane];
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const float *xr = xb + (tg * 8 + t) * (RT_KC * 32) + s4 * 128 + lane;
+                const float x0 = xr[0], x1 = xr[32], x2 = xr[64], x3 = xr[96];
+#pragma unroll
+                for (int r = 0; r < 8; r++) {
+                    float v = acc[r][t];
+                    v = fmaf(w[r].x, x0, v);
+                    v = fmaf(w[r].y, x1, v);
+                    v = fmaf(w[r].z, x2, v);
+                    v = fmaf(w[r].w, x3, v);
+                    acc[r][t] = v;
+                }
+            }
+        }
+    }
+    const int nrows = ne + (a.gate_inp ? 1 : 0);
+#pragma unroll
+    for (int r = 0; r < 8; r++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            float v = acc[r][t];
+            v = v + __shfl_xor(v, 8);  // acc0+acc1 (lanes 0-7), acc2+acc3 (16-23)
+            v = v + __shfl_xor(v, 16); // (acc0+acc1)+(acc2+acc3)
+            v = v + __shfl_xor(v, 4);  // the two 128-bit halves
+            v = v + __shfl_xor(v, 2);  // movehl
+            v = v + __shfl_xor(v, 1);  // movehdup
+            const int row = r0 + rg * 8 + r, tok = t0 + tg * 8 + t;
+            if (lane == ((r * 8 + t) & 31) && row < nrows && tok < T) {
+                if (row < ne) a.logits[(size_t)tok * ne + row] = v;
+                else a.glogit[tok] = v;
+            }
+        }
+}
+
 // ---------------------------------------------------------------------------
 // ops::rms_norm (ops.rs:136-144) of each row of n: ss = dot_f32(g, g) / n in
 // the 32-chain order above, scale = 1 / sqrt(ss + eps), v *= scale * w.  A
@@ -1727,6 +1838,12 @@ hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, i
 
 hipError_t launch_router(const RouterArgs &a, hipStream_t st)
 {
+    if (a.T >= RT_MIN_T && a.E % (32 * RT_KC) == 0) {
+        const int n_tr = (a.n_expert + 1 + RT_ROWS - 1) / RT_ROWS, n_tt = (a.T + RT_TOKS - 1) / RT_TOKS;
+        const int qblocks = a.T * (a.E / 32), nq = (qblocks + 4 * 256 - 1) / (4 * 256);
+        k_router_tiled<<<n_tr * n_tt + nq, 256, 0, st>>>(a, n_tr, n_tt);
+        return hipGetLastError();
+    }
     const int rows = a.n_expert + 1;
     // quantisation workgroups beside the row groups: about one block per thread
     const int qblocks = a.T * (a.E / 32);
