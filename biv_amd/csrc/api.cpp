@@ -407,12 +407,7 @@ int scratch_fit(biv_hip_ctx *ctx, const biv_hip_moe *m, int T)
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.tok_pairs);
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.ids);
     rc = rc ? rc : sc_alloc(ctx, P, &s.dp.wts);
-    rc = rc ? rc : sc_alloc(ctx, biv::n_counters(), &s.counters);
-    if (!rc) {
-        // the finishing-workgroup tickets start at zero; kernels reset them after use
-        hipError_t e = hipMemset(s.counters, 0, sizeof(int) * biv::n_counters());
-        if (e != hipSuccess) rc = hip_fail(ctx, e, "clear counters");
-    }
+    rc = rc ? rc : sc_alloc(ctx, biv::route_work_ints(cap), &s.counters);
     if (rc) {
         scratch_free(ctx);
         return rc;

@@ -56,12 +56,11 @@ struct Dispatch {
 
 // Launchers (kernels.hip).  All enqueue on `st`; none synchronises.
 //
-// A forward is six launches: router (with the quantisation of h); route and
-// dispatch sort; gate/up; quantisation of the intermediate; down; combine.
-// The dispatch sort needs every token routed: the workgroup that finishes
-// routing last does it, found with an integer ticket counter (the result does
-// not depend on which workgroup that is).  The counter starts at zero
-// (cleared when the scratch is allocated) and that workgroup puts it back.
+// A forward is router (with the quantisation of h); route and dispatch
+// sort; gate/up; then down and combine in one launch at decode sizes, or the
+// quantisation of the intermediate, down and combine apart.  Past 16 tokens
+// the dispatch sort is a counting sort over blocks of 16 tokens in three
+// launches (per-block counts with the routing, one scan, the placement).
 
 struct RouterArgs {
     const float *router;   // [n_expert][E], f32 chain layout
@@ -75,9 +74,10 @@ struct RouterArgs {
 };
 // router logits + gate_inp logit + Q8 quantisation of h
 hipError_t launch_router(const RouterArgs &a, hipStream_t st);
-// route every token, then sort the pairs into dispatch order
+// route every token, then sort the pairs into dispatch order (`work`:
+// route_work_ints(T) ints of scratch)
 hipError_t launch_route_sort(const float *logits, int n_expert, int k, int T, int chunk, const Dispatch &dp,
-                             int *counter, hipStream_t st);
+                             int *work, hipStream_t st);
 
 // upper bound of the routed slots of T tokens: one partial slot per expert plus P / chunk full ones
 inline int max_slots(int n_expert, int P, int chunk) { return (n_expert < P ? n_expert : P) + P / chunk; }
@@ -183,6 +183,8 @@ hipError_t launch_q8_mfma_down(const MvArgs &a, hipStream_t st);
 // y = ops::rms_norm(x) of rows x n (y may be x; n a multiple of 32)
 hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, int n, float eps, hipStream_t st);
 
-inline size_t n_counters() { return 1; }
+// ints of the dispatch sort's work area for T tokens (per-block expert
+// counts, then each expert's first position and first slot)
+inline size_t route_work_ints(int T) { return ((size_t)(T + 15) / 16 + 2) * 256; }
 
 } // namespace biv

@@ -135,24 +135,6 @@ __device__ inline void load32(const float *p, float (&v)[32])
     }
 }
 
-// The caller's workgroup takes a ticket on *counter after its threads are
-// done; true in the workgroup whose ticket is total - 1, which then sees every
-// other workgroup's writes and puts the counter back to zero.
-__device__ inline bool finishing_workgroup(int *counter, int total)
-{
-    __shared__ int last;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        const int ticket = atomicAdd(counter, 1);
-        last = ticket == total - 1;
-        if (last) atomicExch(counter, 0);
-    }
-    __syncthreads();
-    if (last) __threadfence();
-    return last;
-}
-
 // ---------------------------------------------------------------------------
 // Router logits (and the shared expert's gate logit, row n_expert) in the
 // order of biv's AVX2 dot_f32 (quant.rs:1177-1207): lane L of a 32-lane half
@@ -635,114 +617,6 @@ __device__ void route_token(const float *__restrict__ logits, int n_expert, int 
 constexpr int MAX_EXPERTS = 256;
 constexpr int RS_THREADS = 1024;
 
-// Inclusive scan of v over the MAX_EXPERTS first threads (all threads call
-// it): a shuffle scan in each of the first four wavefronts, then the wave
-// totals through LDS.
-template <int NT> __device__ inline int scan_experts(int v, int *buf)
-{
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    int x = tid < MAX_EXPERTS ? v : 0;
-#pragma unroll
-    for (int off = 1; off < WAVE; off <<= 1) {
-        const int y = __shfl_up(x, off);
-        if (lane >= off) x += y;
-    }
-    if (tid < MAX_EXPERTS && lane == WAVE - 1) buf[w] = x;
-    __syncthreads();
-    int add = 0;
-    for (int i = 0; i < w && i < MAX_EXPERTS / WAVE; i++) add += buf[i];
-    __syncthreads();
-    return tid < MAX_EXPERTS ? x + add : 0;
-}
-
-template <int NT>
-__device__ void sort_pairs(const int *__restrict__ ids, const float *__restrict__ wts, int n_expert, int k, int T,
-                           int chunk, const Dispatch &dp)
-{
-    static_assert(NT >= MAX_EXPERTS, "one thread per expert");
-    constexpr int TPC_MAX = NT < 256 ? NT : 256; // tokens placed per round
-    __shared__ int cnt[MAX_EXPERTS];
-    __shared__ int scan[MAX_EXPERTS];
-    __shared__ int run[MAX_EXPERTS];
-    __shared__ unsigned bm[MAX_EXPERTS][TPC_MAX / 32];
-    __shared__ int sid[NT];
-    __shared__ float sw[NT];
-    const int tid = threadIdx.x;
-    const int P = T * k;
-    for (int e = tid; e < MAX_EXPERTS; e += NT) {
-        cnt[e] = 0;
-        run[e] = 0;
-    }
-    __syncthreads();
-    for (int i = tid; i < P; i += NT) atomicAdd(&cnt[ids[i]], 1); // ids < n_expert (route_token)
-    __syncthreads();
-    // offsets of the experts' pairs, and of their slots
-    const int c = tid < n_expert ? cnt[tid] : 0;
-    const int nsl = (c + chunk - 1) / chunk;
-    const int pos_incl = scan_experts<NT>(c, scan);
-    const int sl_incl = scan_experts<NT>(nsl, scan);
-    __shared__ int n_used;
-    __shared__ int sfirst[MAX_EXPERTS];
-    if (tid < n_expert) {
-        const int beg = pos_incl - c;
-        for (int j = 0; j < nsl; j++) {
-            int4 *rec = reinterpret_cast<int4 *>(&dp.slots[sl_incl - nsl + j]);
-            rec[0] = make_int4(tid, beg + j * chunk, min(chunk, c - j * chunk), 0);
-        }
-        cnt[tid] = beg; // from here on: the expert's first position
-        sfirst[tid] = sl_incl - nsl;
-    }
-    if (tid == MAX_EXPERTS - 1) n_used = sl_incl;
-    __syncthreads();
-    // the slots past the used ones are empty, so that a consumer needs one record
-    for (int u = n_used + tid; u < dp.slot_cap; u += NT)
-        reinterpret_cast<int4 *>(&dp.slots[u])[0] = make_int4(0, 0, 0, 0);
-    // place the pairs, tpc tokens at a time, one thread per pair: a pair's
-    // place among its expert's pairs is `run` (earlier rounds) plus the
-    // earlier tokens of this round with that expert, read from a bitmap
-    const int tpc = min(NT / k, TPC_MAX);
-    const int nw = (tpc + 31) / 32;
-    for (int t0 = 0; t0 < T; t0 += tpc) {
-        const int nt = min(tpc, T - t0), np = nt * k;
-        for (int i = tid; i < np; i += NT) {
-            sid[i] = ids[(size_t)t0 * k + i];
-            sw[i] = wts[(size_t)t0 * k + i];
-        }
-        for (int i = tid; i < MAX_EXPERTS * nw; i += NT) bm[i / nw][i % nw] = 0u;
-        __syncthreads();
-        const int tl = tid / k;
-        const unsigned bit = 1u << (tl & 31);
-        int e = 0;
-        if (tid < np) {
-            e = sid[tid];
-            atomicOr(&bm[e][tl >> 5], bit);
-        }
-        __syncthreads();
-        if (tid < np) {
-            int r = run[e] + __popc(bm[e][tl >> 5] & (bit - 1));
-            for (int w = 0; w < (tl >> 5); w++) r += __popc(bm[e][w]);
-            const int p = cnt[e] + r;
-            const int t = t0 + tl;
-            dp.pair_tok[p] = t;
-            if (r % chunk < SLOT_TOKS) dp.slots[sfirst[e] + r / chunk].tok[r % chunk] = t;
-            dp.pair_exp[p] = e;
-            dp.pair_w[p] = sw[tid];
-            // positions ascend with the expert id: the pair's place among the
-            // token's k is the number of its experts below e
-            int rank = 0;
-            for (int j2 = 0; j2 < k; j2++) rank += sid[tl * k + j2] < e;
-            dp.tok_pairs[(size_t)t * k + rank] = p;
-        }
-        __syncthreads();
-        if (tid < MAX_EXPERTS) {
-            int add = 0;
-            for (int w = 0; w < nw; w++) add += __popc(bm[tid][w]);
-            run[tid] += add;
-        }
-        __syncthreads();
-    }
-}
-
 // LDS writes of this wavefront visible to all its lanes
 __device__ inline void wave_lds_sync()
 {
@@ -827,14 +701,112 @@ __device__ void sort_pairs_wave(const int *ids, const float *wts, int n_expert, 
     }
 }
 
+// The counting sort past one workgroup (the `routed` lists of
+// model.rs:866-873, Metal's moe_sort): tokens in blocks of RS_WAVES.
+// route_block_counts: block b's per-expert pair counts, work[b * 256 + e].
+// k_dispatch_scan (one workgroup): turns them, in place, into each block's
+// first rank within the expert; each expert's first dispatch position and
+// first slot (work[nb * 256 + e], work[(nb + 1) * 256 + e]); the slot
+// records.  k_dispatch_place: every pair to its position, a pair's place
+// among its expert's pairs being its block's first rank plus the earlier
+// tokens of its block with that expert (a token bitmap in LDS).  No atomics
+// on values: the order is that of the single-workgroup sort.
+constexpr int RB_TOKS = RS_THREADS / WAVE; // tokens per block
+
+__device__ inline void block_masks(const int *ids, int n_expert, int k, int T, int b, unsigned *mask)
+{
+    const int t0 = b * RB_TOKS, nt = min(RB_TOKS, T - t0);
+    for (int e = threadIdx.x; e < MAX_EXPERTS; e += blockDim.x) mask[e] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < nt * k; i += blockDim.x) atomicOr(&mask[ids[(size_t)t0 * k + i]], 1u << (i / k));
+    __syncthreads();
+}
+
+__device__ void route_block_counts(const int *ids, int n_expert, int k, int T, int b, int *work)
+{
+    __shared__ unsigned mask[MAX_EXPERTS];
+    block_masks(ids, n_expert, k, T, b, mask);
+    for (int e = threadIdx.x; e < MAX_EXPERTS; e += blockDim.x) work[(size_t)b * MAX_EXPERTS + e] = __popc(mask[e]);
+}
+
+__global__ __launch_bounds__(MAX_EXPERTS) void k_dispatch_scan(int n_expert, int nb, int chunk, Dispatch dp, int *work)
+{
+    const int e = threadIdx.x, lane = e & (WAVE - 1), w = e >> 6;
+    // the column of block counts, 16 loads in flight at a time
+    int run = 0;
+    for (int b0 = 0; b0 < nb; b0 += 16) {
+        int v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = b0 + j < nb ? work[(size_t)(b0 + j) * MAX_EXPERTS + e] : 0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            if (b0 + j < nb) work[(size_t)(b0 + j) * MAX_EXPERTS + e] = run;
+            run += v[j];
+        }
+    }
+    const int tot = e < n_expert ? run : 0, nsl = (tot + chunk - 1) / chunk;
+    // exclusive scans over the experts of the pair and slot totals
+    __shared__ int wsum[2][MAX_EXPERTS / WAVE];
+    int x = tot, y = nsl;
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+        const int xs = __shfl_up(x, off), ys = __shfl_up(y, off);
+        if (lane >= off) {
+            x += xs;
+            y += ys;
+        }
+    }
+    if (lane == WAVE - 1) {
+        wsum[0][w] = x;
+        wsum[1][w] = y;
+    }
+    __syncthreads();
+    int px = 0, py = 0;
+    for (int i = 0; i < w; i++) {
+        px += wsum[0][i];
+        py += wsum[1][i];
+    }
+    const int first = px + x - tot, sfirst = py + y - nsl;
+    int n_used = 0;
+    for (int i = 0; i < MAX_EXPERTS / WAVE; i++) n_used += wsum[1][i];
+    work[(size_t)nb * MAX_EXPERTS + e] = first;
+    work[(size_t)(nb + 1) * MAX_EXPERTS + e] = sfirst;
+    for (int j = 0; j < nsl; j++)
+        reinterpret_cast<int4 *>(&dp.slots[sfirst + j])[0] = make_int4(e, first + j * chunk, min(chunk, tot - j * chunk), 0);
+    for (int u = n_used + e; u < dp.slot_cap; u += MAX_EXPERTS) reinterpret_cast<int4 *>(&dp.slots[u])[0] = make_int4(0, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void k_dispatch_place(int n_expert, int k, int T, int nb, int chunk, Dispatch dp,
+                                                        const int *work)
+{
+    __shared__ unsigned mask[MAX_EXPERTS];
+    const int b = blockIdx.x, t0 = b * RB_TOKS, nt = min(RB_TOKS, T - t0);
+    block_masks(dp.ids, n_expert, k, T, b, mask);
+    const int *base = work + (size_t)b * MAX_EXPERTS, *first = work + (size_t)nb * MAX_EXPERTS,
+              *sfirst = work + (size_t)(nb + 1) * MAX_EXPERTS;
+    for (int i = threadIdx.x; i < nt * k; i += blockDim.x) {
+        const int tl = i / k, t = t0 + tl;
+        const int e = dp.ids[(size_t)t0 * k + i];
+        const int r = base[e] + __popc(mask[e] & ((1u << tl) - 1u)); // rank among the expert's pairs
+        const int p = first[e] + r;
+        dp.pair_tok[p] = t;
+        dp.pair_exp[p] = e;
+        dp.pair_w[p] = dp.wts[(size_t)t0 * k + i];
+        int rank = 0; // among the token's experts, ascending id
+        for (int j = 0; j < k; j++) rank += dp.ids[(size_t)t * k + j] < e;
+        dp.tok_pairs[(size_t)t * k + rank] = p;
+        if (r % chunk < SLOT_TOKS) dp.slots[sfirst[e] + r / chunk].tok[r % chunk] = t;
+    }
+}
+
 // One wavefront per token routes it, then the pairs are sorted: with a
 // single workgroup (T <= RS_WAVES, so at most 4 * WAVE pairs as k <= 16) by
-// one wavefront from LDS, else by the workgroup that finishes routing last,
-// from global memory.
+// one wavefront from LDS, else by the counting sort above (each routing
+// workgroup counts its block; k_dispatch_scan and k_dispatch_place follow).
 constexpr int RS_WAVES = RS_THREADS / WAVE;
 
 __global__ __launch_bounds__(RS_THREADS) void k_route_sort(const float *__restrict__ logits, int n_expert, int k,
-                                                           int T, int chunk, Dispatch dp, int *counter)
+                                                           int T, int chunk, Dispatch dp, int *work)
 {
     __shared__ float es[RS_WAVES][MAX_EXPERTS];
     __shared__ int lds_ids[RS_WAVES * 16];
@@ -851,8 +823,11 @@ __global__ __launch_bounds__(RS_THREADS) void k_route_sort(const float *__restri
         if (wave == 0) sort_pairs_wave(lds_ids, lds_wts, n_expert, k, T, chunk, dp, cnt, first, sfirst);
         return;
     }
-    if (!finishing_workgroup(counter, gridDim.x)) return;
-    sort_pairs<RS_THREADS>(dp.ids, dp.wts, n_expert, k, T, chunk, dp);
+    if (single) return;
+    // past one workgroup: this block's expert counts for the counting sort
+    // (k_dispatch_scan, k_dispatch_place); block b holds tokens 16 b .. 16 b + 15
+    __syncthreads();
+    route_block_counts(dp.ids, n_expert, k, T, blockIdx.x, work);
 }
 
 // ---------------------------------------------------------------------------
@@ -1869,12 +1844,16 @@ hipError_t launch_router(const RouterArgs &a, hipStream_t st)
 }
 
 hipError_t launch_route_sort(const float *logits, int n_expert, int k, int T, int chunk, const Dispatch &dp,
-                             int *counter, hipStream_t st)
+                             int *work, hipStream_t st)
 {
     // a single workgroup routes and sorts in LDS while every token has its wavefront
     const int groups = T <= RS_WAVES ? 1 : (T + RS_WAVES - 1) / RS_WAVES;
     const int threads = groups == 1 ? WAVE * T : RS_THREADS; // a wavefront per token
-    k_route_sort<<<groups, threads, 0, st>>>(logits, n_expert, k, T, chunk, dp, counter);
+    k_route_sort<<<groups, threads, 0, st>>>(logits, n_expert, k, T, chunk, dp, work);
+    if (groups > 1) {
+        k_dispatch_scan<<<1, MAX_EXPERTS, 0, st>>>(n_expert, groups, chunk, dp, work);
+        k_dispatch_place<<<groups, 256, 0, st>>>(n_expert, k, T, groups, chunk, dp, work);
+    }
     return hipGetLastError();
 }
 
