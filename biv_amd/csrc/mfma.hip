@@ -298,6 +298,23 @@ constexpr int QRT = 2;           // 16-row tiles of a wave
 constexpr int Q_ROWS_WG = QW * 16 * QRT;
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Four small integers as four exact f16 (two dwords).  Each byte u (0..255)
+// becomes the f16 with bits 0x64uu, i.e. 1024 + u, and BIAS is taken off
+// (exact: every value is an integer below 2048).  Signed int8 quants come
+// in as q ^ 0x80 = q + 128 with BIAS 1152; nibbles 0..15 with BIAS 1024.
+template <int BIAS> __device__ __forceinline__ uint2 bytes_to_f16x4(uint32_t u)
+{
+    const uint32_t r0 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t r1 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const f16x2 bias = {(_Float16)BIAS, (_Float16)BIAS};
+    const f16x2 h0 = __builtin_bit_cast(f16x2, r0) - bias, h1 = __builtin_bit_cast(f16x2, r1) - bias;
+    return make_uint2(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1));
+}
+__device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t q) { return bytes_to_f16x4<1152>(q ^ 0x80808080u); }
 
 __device__ inline float f16_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
@@ -461,13 +478,16 @@ __global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
 // fma(float(word dot), w_scale(b) * d_x(b), acc); then the chains are summed
 // in a fixed tree, and Q4_K subtracts its mins term last (the chain kernels
 // in kernels.hip do exactly this on the vector ALU).  Here
-// v_mfma_i32_16x16x32_i8 produces the word dots: its A operand is the block
-// of two input rows, masked so that A row 8 tt + l keeps only word l of
-// input row tt; its B operand is the block of 16 weight rows (8 gate rows,
-// then the same 8 rows of up) as int8 (Q4_K: the block's nibbles, 0..15).
-// D row 8 tt + l, column n is then the word-l dot of input row tt and weight
-// row n, exactly.  The vector ALU does what remains, in the reference's
-// order: convert, fma into the chain, tree, mins, SwiGLU.
+// v_mfma_f32_16x16x32_f16 produces the word dots, already as f32: its A
+// operand is the block of two input rows, masked so that A row 8 tt + l
+// keeps only word l of input row tt; its B operand is the block of 16 weight
+// rows (8 gate rows, then the same 8 rows of up).  Both hold the quants
+// (Q4_K: nibbles 0..15) as f16, which is exact for integers this small;
+// every product is exact and every partial sum an integer below 2^17, so D
+// row 8 tt + l, column n is the word-l dot of input row tt and weight row n,
+// exactly, and equal to the reference's float(int32 word dot) without a
+// convert.  The vector ALU does what remains, in the reference's order: fma
+// into the chain, tree, mins, SwiGLU.
 //
 // D of an MFMA: lane (n, kq) holds column n and A rows 4 kq .. 4 kq + 3,
 // i.e. input row kq / 2 of the pair, words 4 (kq & 1) .. + 3: eight chains
@@ -481,8 +501,8 @@ __global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
 // Weight operands of the exact kernel.  A step covers the blocks 8 g + pi +
 // 2 j (j = 0..3) of one parity (Q8_0: a half-group) or both parities (Q4_K:
 // super-block g, whose nibble bytes serve both).  operand(w, pi, j) is the
-// lane's 8 bytes of block 8 g + pi + 2 j; scale(w, pi, j) its f32 weight
-// scale as the reference forms it.
+// lane's 8 quants of block 8 g + pi + 2 j as exact f16; scale(w, pi, j)
+// its f32 weight scale as the reference forms it.
 template <int TY, int K> struct GuW;
 
 // Q8_0 (chain layout: unit 16 g + 8 pi + w holds word w of the blocks
@@ -506,9 +526,10 @@ template <int K> struct GuW<T_Q8_0, K> {
         w.q[1] = wq[16 * g + 8 * pi + 1];
         w.s = wsc[(pi * (K / 64) + 4 * g) / 4];
     }
-    __device__ static long operand(const Step &w, int pi, int j)
+    __device__ static uint4 operand(const Step &w, int pi, int j)
     {
-        return (long)((uint64_t)w.q[0][j] | (uint64_t)w.q[1][j] << 32);
+        const uint2 lo = i8x4_to_f16x4(w.q[0][j]), hi = i8x4_to_f16x4(w.q[1][j]);
+        return make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
     __device__ static float scale(const Step &w, int pi, int j)
     {
@@ -538,10 +559,11 @@ template <int K> struct GuW<T_Q4K, K> {
         w.q[1] = wq[8 * g + 1];
         w.hd = whd[g];
     }
-    __device__ static long operand(const Step &w, int pi, int j)
+    __device__ static uint4 operand(const Step &w, int pi, int j)
     {
-        const uint32_t lo = (w.q[0][j] >> (4 * pi)) & 0x0F0F0F0Fu, hi = (w.q[1][j] >> (4 * pi)) & 0x0F0F0F0Fu;
-        return (long)((uint64_t)lo | (uint64_t)hi << 32);
+        const uint2 lo = bytes_to_f16x4<1024>((w.q[0][j] >> (4 * pi)) & 0x0F0F0F0Fu);
+        const uint2 hi = bytes_to_f16x4<1024>((w.q[1][j] >> (4 * pi)) & 0x0F0F0F0Fu);
+        return make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
     __device__ static float scale(const Step &w, int pi, int j)
     {
@@ -554,6 +576,12 @@ template <int K> struct GuW<T_Q4K, K> {
 };
 
 template <int TY, int K, bool DUMP>
+#ifndef GU_EXACT_AJ
+#define GU_EXACT_AJ 2 // blocks per LDS read group, Q8_0
+#endif
+#ifndef GU_EXACT_AJ_Q4K
+#define GU_EXACT_AJ_Q4K 1 // and Q4_K (fewer registers)
+#endif
 __global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
 {
     using W = GuW<TY, K>;
@@ -562,14 +590,13 @@ __global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
     constexpr int DSTR = NB + 4;     // staged scales [row][q8_scale order]: floats (16-byte aligned rows)
     constexpr bool Q4K = TY == T_Q4K;
     static_assert(QT % 2 == 0, "pairs of input rows");
-    // The A operands, masked in advance: for input row i, block b and A row
-    // word l, the 8 bytes lane kq = l / 2 supplies ({word l, 0} for even l,
-    // {0, word l} for odd l), at ((i * NB + b) * 8 + l) * 8.  The lanes whose
-    // A row word is not theirs read zeros from a region past the operands,
-    // as long as every offset a step adds (< (NB + 8) * 64 bytes).
-    constexpr int XOPS = QT * NB * 8; // 8-byte operands
-    constexpr int XZERO = (NB + 8) * 8;
-    __shared__ uint2 xop_s[XOPS + XZERO];
+    constexpr int AJ = Q4K ? GU_EXACT_AJ_Q4K : GU_EXACT_AJ;          // blocks per A read group
+    // The input rows' words as exact f16: word l of block b of input row i
+    // (four values, 8 bytes) at xop_s[i * XRS + 8 b + l].  Rows are XRS
+    // entries apart, 64 bytes more than their words, so that the two rows of
+    // a pair sit in different LDS banks.
+    constexpr int XRS = NB * 8 + 8;
+    __shared__ uint2 xop_s[QT * XRS];
     __shared__ float xd_s[QT * DSTR];
     __shared__ float xs_s[Q4K ? QT * DSTR : 1]; // Q4_K: d * sum(q) of each block, for the mins
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -614,10 +641,9 @@ __global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int b = 8 * g + pi + 2 * j;
-                xop_s[(i * NB + b) * 8 + l] = (l & 1) ? make_uint2(0u, v[j]) : make_uint2(v[j], 0u);
+                xop_s[i * XRS + b * 8 + l] = i8x4_to_f16x4(v[j]);
             }
         }
-        for (int idx = tid; idx < XZERO; idx += QNTH) xop_s[XOPS + idx] = make_uint2(0u, 0u);
         for (int idx = tid; idx < QT * NB; idx += QNTH) {
             const int i = idx / NB, bs = idx % NB;
             const int ti = min(i, cnt - 1);
@@ -628,12 +654,17 @@ __global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
     }
     __syncthreads();
     // the A operand: A row 8 tt + l keeps word l of input row tt, which lane
-    // kq = l / 2 supplies; the other lanes read zeros (a base that does not
-    // move with the pair)
+    // kq = l / 2 holds in its low half (l even) or high half (l odd); every
+    // other half of every lane is zero.  The registers start at zero and the
+    // lanes load only their own half (reads under an exec mask), so the
+    // zeros stay and no lane reads LDS for them.
     const int tt = (n >> 3), l = n & 7;
     const bool mine = (l >> 1) == kq;
-    const uint2 *xbase = mine ? xop_s + tt * NB * 8 + l : xop_s + XOPS;
-    const int xpair = mine ? 2 * NB * 8 : 0; // operands from one pair to the next
+    const uint64_t mlo = __ballot(mine && !(l & 1)), mhi = __ballot(mine && (l & 1));
+    const uint32_t xa0 = (uint32_t)reinterpret_cast<uintptr_t>(xop_s + tt * XRS + l);
+    uint64_t alo[AJ], ahi[AJ];
+#pragma unroll
+    for (int j = 0; j < AJ; j++) alo[j] = ahi[j] = 0ull;
     // this lane's D: input row kq / 2 of the pair, chains (pi, 4 (kq & 1) + jj)
     const int drow = kq >> 1;
     float acc[NPR][2][4];
@@ -647,43 +678,76 @@ __global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
     // constant: it picks the chain accumulators)
     auto compute = [&](int g, auto pi_c, const typename W::Step &w) {
         constexpr int pi = decltype(pi_c)::value;
-        float dw[4];
-        long wo[4];
+        // AJ blocks at a time: their weight operands converted once, then
+        // met with every pair of the slot
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            dw[j] = W::scale(w, pi, j);
-            wo[j] = W::operand(w, pi, j);
-        }
+        for (int j0 = 0; j0 < 4; j0 += AJ) {
+            float dw[AJ];
+            f16x8 wo[AJ];
 #pragma unroll
-        for (int p = 0; p < NPR; p++) {
-            if (2 * p < cnt) { // uniform
-                // A: input row 2 p + tt's masked operands of blocks 8 g + pi + 2 j
-                const uint2 *xr = xbase + p * xpair + (8 * g + pi) * 8;
-                // d_x of the 4 blocks for this lane's D row (input row 2 p + drow)
-                const float4 dx = *reinterpret_cast<const float4 *>(xd_s + (2 * p + drow) * DSTR + pi * (K / 64) + 4 * g);
-                const float dxs[4] = {dx.x, dx.y, dx.z, dx.w};
+            for (int jr = 0; jr < AJ; jr++) {
+                dw[jr] = W::scale(w, pi, j0 + jr);
+                wo[jr] = __builtin_bit_cast(f16x8, W::operand(w, pi, j0 + jr));
+            }
+            // this lane's words of pair 0, blocks 8 g + pi + 2 j0 ..
+            const uint32_t xa = xa0 + ((8 * g + pi) * 8 + 16 * j0) * 8;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const uint2 xv = xr[16 * j];
-                    const long xo = (long)((uint64_t)xv.x | (uint64_t)xv.y << 32);
-                    const i32x4 z = {0, 0, 0, 0};
-                    const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo, wo[j], z, 0, 0, 0);
-                    const float sb = dw[j] * dxs[j]; // w_scale * d_x, as the reference
+            for (int p = 0; p < NPR; p++) {
+                if (2 * p < cnt) { // uniform
+                    // d_x of the blocks for this lane's D row (input row 2 p + drow)
+                    const float *dxr = xd_s + (2 * p + drow) * DSTR + pi * (K / 64) + 4 * g + j0;
+                    float dxs[AJ];
 #pragma unroll
-                    for (int jj = 0; jj < 4; jj++) acc[p][pi][jj] = __builtin_fmaf((float)d[jj], sb, acc[p][pi][jj]);
-                    if (DUMP) {
-                        // the block's int32: the sum of its 8 word dots
-                        int bs = d[0] + d[1] + d[2] + d[3];
-                        bs += __shfl_xor(bs, 16);
-                        int32_t *dump = n < 8 ? a.dump_a : a.dump_b;
-                        const int i = 2 * p + drow;
-                        if (dump && !(kq & 1) && i < cnt)
-                            dump[((size_t)(beg + i) * rows + orow) * NB + 8 * g + pi + 2 * j] = bs;
+                    for (int jr = 0; jr < AJ; jr++) dxs[jr] = dxr[jr];
+                    // the A words: low halves under one exec mask, high halves
+                    // under the other, exec restored, then a wait for them
+                    constexpr int PO = 2 * XRS * 8; // bytes from pair to pair
+                    uint64_t ex;
+                    if constexpr (AJ == 1) {
+                        asm volatile("s_mov_b64 %0, exec\n\ts_mov_b64 exec, %3\n\t"
+                                     "ds_read_b64 %1, %5 offset:%6\n\t"
+                                     "s_mov_b64 exec, %4\n\t"
+                                     "ds_read_b64 %2, %5 offset:%6\n\t"
+                                     "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
+                                     : "=&s"(ex), "+v"(alo[0]), "+v"(ahi[0])
+                                     : "s"(mlo), "s"(mhi), "v"(xa), "i"(PO * p)
+                                     : "memory");
+                    } else {
+                        static_assert(AJ == 2, "AJ");
+                        asm volatile("s_mov_b64 %0, exec\n\ts_mov_b64 exec, %5\n\t"
+                                     "ds_read_b64 %1, %7 offset:%8\n\t"
+                                     "ds_read_b64 %2, %7 offset:%9\n\t"
+                                     "s_mov_b64 exec, %6\n\t"
+                                     "ds_read_b64 %3, %7 offset:%8\n\t"
+                                     "ds_read_b64 %4, %7 offset:%9\n\t"
+                                     "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
+                                     : "=&s"(ex), "+v"(alo[0]), "+v"(alo[1]), "+v"(ahi[0]), "+v"(ahi[1])
+                                     : "s"(mlo), "s"(mhi), "v"(xa), "i"(PO * p), "i"(PO * p + 128)
+                                     : "memory");
+                    }
+#pragma unroll
+                    for (int jr = 0; jr < AJ; jr++) {
+                        const int j = j0 + jr;
+                        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                        const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(f16x8, make_ulonglong2(alo[jr], ahi[jr])), wo[jr], z, 0, 0, 0);
+                        const float sb = dw[jr] * dxs[jr]; // w_scale * d_x, as the reference
+#pragma unroll
+                        for (int jj = 0; jj < 4; jj++) acc[p][pi][jj] = __builtin_fmaf(d[jj], sb, acc[p][pi][jj]);
+                        if (DUMP) {
+                            // the block's int32: the sum of its 8 word dots
+                            int bs = (int)d[0] + (int)d[1] + (int)d[2] + (int)d[3];
+                            bs += __shfl_xor(bs, 16);
+                            int32_t *dump = n < 8 ? a.dump_a : a.dump_b;
+                            const int i = 2 * p + drow;
+                            if (dump && !(kq & 1) && i < cnt)
+                                dump[((size_t)(beg + i) * rows + orow) * NB + 8 * g + pi + 2 * j] = bs;
+                        }
                     }
                 }
+                // one pair's LDS reads and MFMA results live at a time
+                __builtin_amdgcn_sched_barrier(0);
             }
-            // one pair's LDS reads and MFMA results live at a time
-            __builtin_amdgcn_sched_barrier(0);
         }
     };
     auto step = [&](int h, const typename W::Step &w) {
