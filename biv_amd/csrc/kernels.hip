@@ -1577,6 +1577,50 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a)
     *po = a.add ? *po + o : o;
 }
 
+// The same combine, four columns per thread and the k routes known at
+// compile time, so that every load of a thread (the token's pair records,
+// its k + 1 y rows, the residual) is issued before the first FMA: grid
+// (E / 1024, T).  Each column runs the same FMA sequence as above.
+template <int KK> __global__ __launch_bounds__(256) void k_combine4(CombineArgs a)
+{
+    const int t = blockIdx.y;
+    const int c = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (c >= a.E) return;
+    int p[KK];
+    float w[KK];
+    float4 y[KK];
+#pragma unroll
+    for (int j = 0; j < KK; j++) p[j] = a.dp.tok_pairs[(size_t)t * KK + j];
+#pragma unroll
+    for (int j = 0; j < KK; j++) {
+        w[j] = a.dp.pair_w[p[j]];
+        y[j] = *reinterpret_cast<const float4 *>(a.y + (size_t)p[j] * a.E + c);
+    }
+    float4 ys = make_float4(0.0f, 0.0f, 0.0f, 0.0f), r = ys;
+    float g = 0.0f;
+    if (a.has_shared) {
+        ys = *reinterpret_cast<const float4 *>(a.y + (size_t)(a.P + t) * a.E + c);
+        g = sigmoid(a.glogit[t]);
+    }
+    float4 *po = reinterpret_cast<float4 *>(a.out + (size_t)t * a.E + c);
+    if (a.add) r = *po;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int j = 0; j < KK; j++) {
+        o.x = fmaf(w[j], y[j].x, o.x);
+        o.y = fmaf(w[j], y[j].y, o.y);
+        o.z = fmaf(w[j], y[j].z, o.z);
+        o.w = fmaf(w[j], y[j].w, o.w);
+    }
+    if (a.has_shared) {
+        o.x = fmaf(g, ys.x, o.x);
+        o.y = fmaf(g, ys.y, o.y);
+        o.z = fmaf(g, ys.z, o.z);
+        o.w = fmaf(g, ys.w, o.w);
+    }
+    *po = a.add ? make_float4(r.x + o.x, r.y + o.y, r.z + o.z, r.w + o.w) : o;
+}
+
 // ---------------------------------------------------------------------------
 // Down and combine in one launch, for decode sizes (every expert's pairs in
 // one slot).  A workgroup owns RB output rows and computes them for every
@@ -1868,6 +1912,10 @@ hipError_t launch_combine(const float *y, const Dispatch &dp, const float *glogi
                           int E, float *out, int add, hipStream_t st)
 {
     CombineArgs c{y, dp, glogit, out, T, P, k, E, has_shared, add};
+    if (k == 8 && E % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+        k_combine4<8><<<dim3((E + 1023) / 1024, T), 256, 0, st>>>(c);
+        return hipGetLastError();
+    }
     dim3 grid((E + 255) / 256, T);
     k_combine<<<grid, 256, 0, st>>>(c);
     return hipGetLastError();
