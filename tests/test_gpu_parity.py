@@ -276,6 +276,35 @@ def test_kquant_prefill(orc, engine, T):
     full_parity(orc, engine, layer, moe, h, block_dots=T == 64, min_exact=0.0)
 
 
+def _full_size(orc, moe, layer, h, exact_ids=True):
+    T = h.shape[0]
+    ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
+    got, t = moe.ffn_taps(h, dots=False)
+    if orc.detect_level() >= orc.AVX2:
+        assert np.array_equal(t["logits"].view(np.uint32), logits.view(np.uint32)), "router logits differ"
+    assert np.array_equal(t["ids"], ids), "top-k ids differ"
+    check_dispatch(t, ids, T, layer.k)
+    check_output(ref, got, min_exact=0.0)
+    again = moe.ffn(h)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "not bit-identical run to run"
+
+
+def test_kquant_full_size_2048(orc, engine):
+    """configs[3] at its full size: 256 experts, Q4_K gate/up and Q6_K down,
+    T = 2048 (the matrix-core kernels, exact Q4_K gate/up)."""
+    print("case kquant full T=2048", flush=True)
+    layer, moe = layer_for(engine, seed=33, types=(Q4K, Q4K, Q6K))
+    _full_size(orc, moe, layer, synth.make_tokens(2048, 2048))
+
+
+def test_bf16_full_size_4096(orc, engine):
+    """configs[4]'s layer at its full size: 256 BF16 experts, T = 4096 (bf16
+    MFMA grouped GEMM on hi/lo halves of the f32 activations)."""
+    print("case bf16 full T=4096", flush=True)
+    layer, moe = layer_for(engine, seed=2, types=(BF16, BF16, BF16))
+    _full_size(orc, moe, layer, synth.make_tokens(4096, 4096))
+
+
 def test_mixed_shared_types_prefill(orc, engine):
     """Q4_K routed and Q8_0 shared gate/up at T = 70: two matrix-core launches."""
     print("case mixed shared prefill", flush=True)
