@@ -230,20 +230,30 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
 }
 
 // The router at prefill sizes, register-blocked: each 32-lane half wave runs
-// chain L of dot_f32 for 8 rows x 8 tokens (64 accumulators), so a value read
-// from LDS feeds 8 FMAs rather than one.  A workgroup (8 half waves) takes 16
-// rows x 32 tokens.  Both operands go straight from global memory into LDS,
+// chain L of dot_f32 for RB rows x 8 tokens (8 RB accumulators), so a value
+// read from LDS feeds several FMAs rather than one.  A workgroup (8 half
+// waves) takes 2 RB rows x 32 tokens.  Both operands go straight from global memory into LDS,
 // RT_KC steps of 32 elements at a time: the router
 // rows as stored (f32 chain layout: lane L's four steps in one 16-byte word),
 // the tokens row-major (lane L reads element 32 s + L, conflict-free), into
 // two buffers, one stage ahead of the compute.  Per (row, token) every FMA is the
 // reference's, in its order, then the same tree: the logits carry k_router's
 // bits.
-constexpr int RT_ROWS = 16, RT_TOKS = 32, RT_KC = 4; // RT_KC steps of 32 elements per stage
-constexpr int RT_MIN_T = 64;                          // tokens from which launch_router takes it
+// RB rows per half wave: 8 (16-row tiles) for long chunks; 4 (8-row tiles,
+// twice the workgroups) up to BIV_RT_RB4_T tokens, where 16-row tiles leave
+// about one wave per SIMD.
+constexpr int RT_TOKS = 32, RT_KC = 4; // RT_KC steps of 32 elements per stage
+#ifndef BIV_RT_MIN_T
+#define BIV_RT_MIN_T 256
+#endif
+constexpr int RT_MIN_T = BIV_RT_MIN_T; // tokens from which launch_router takes it
+#ifndef BIV_RT_RB4_T
+#define BIV_RT_RB4_T 512
+#endif
 
-__global__ __launch_bounds__(256) void k_router_tiled(RouterArgs a, int n_tr, int n_tt)
+template <int RB> __global__ __launch_bounds__(256) void k_router_tiled(RouterArgs a, int n_tr, int n_tt)
 {
+    constexpr int RT_ROWS = 2 * RB;
     const int E = a.E, ne = a.n_expert, T = a.T, tid = threadIdx.x;
     const int tile = blockIdx.x;
     if (tile >= n_tr * n_tt) {
@@ -285,9 +295,9 @@ __global__ __launch_bounds__(256) void k_router_tiled(RouterArgs a, int n_tr, in
                 &Xl[b][q * 256 + wv * WAVE]);
         }
     };
-    float acc[8][8];
+    float acc[RB][8];
 #pragma unroll
-    for (int r = 0; r < 8; r++)
+    for (int r = 0; r < RB; r++)
 #pragma unroll
         for (int t = 0; t < 8; t++) acc[r][t] = 0.0f;
     const int nc = E / 32 / RT_KC;
@@ -302,15 +312,15 @@ __global__ __launch_bounds__(256) void k_router_tiled(RouterArgs a, int n_tr, in
         const float *xb = reinterpret_cast<const float *>(&Xl[b][0]);
 #pragma unroll
         for (int s4 = 0; s4 < RT_KC / 4; s4++) {
-            float4 w[8];
+            float4 w[RB];
 #pragma unroll
-            for (int r = 0; r < 8; r++) w[r] = Wl[b][(rg * 8 + r) * WP + s4 * 32 + lane];
+            for (int r = 0; r < RB; r++) w[r] = Wl[b][(rg * RB + r) * WP + s4 * 32 + lane];
 #pragma unroll
             for (int t = 0; t < 8; t++) {
                 const float *xr = xb + (tg * 8 + t) * (RT_KC * 32) + s4 * 128 + lane;
                 const float x0 = xr[0], x1 = xr[32], x2 = xr[64], x3 = xr[96];
 #pragma unroll
-                for (int r = 0; r < 8; r++) {
+                for (int r = 0; r < RB; r++) {
                     float v = acc[r][t];
                     v = fmaf(w[r].x, x0, v);
                     v = fmaf(w[r].y, x1, v);
@@ -323,7 +333,7 @@ __global__ __launch_bounds__(256) void k_router_tiled(RouterArgs a, int n_tr, in
     }
     const int nrows = ne + (a.gate_inp ? 1 : 0);
 #pragma unroll
-    for (int r = 0; r < 8; r++)
+    for (int r = 0; r < RB; r++)
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             float v = acc[r][t];
@@ -332,7 +342,7 @@ __global__ __launch_bounds__(256) void k_router_tiled(RouterArgs a, int n_tr, in
             v = v + __shfl_xor(v, 4);  // the two 128-bit halves
             v = v + __shfl_xor(v, 2);  // movehl
             v = v + __shfl_xor(v, 1);  // movehdup
-            const int row = r0 + rg * 8 + r, tok = t0 + tg * 8 + t;
+            const int row = r0 + rg * RB + r, tok = t0 + tg * 8 + t;
             if (lane == ((r * 8 + t) & 31) && row < nrows && tok < T) {
                 if (row < ne) a.logits[(size_t)tok * ne + row] = v;
                 else a.glogit[tok] = v;
@@ -1858,9 +1868,11 @@ hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, i
 hipError_t launch_router(const RouterArgs &a, hipStream_t st)
 {
     if (a.T >= RT_MIN_T && a.E % (32 * RT_KC) == 0) {
-        const int n_tr = (a.n_expert + 1 + RT_ROWS - 1) / RT_ROWS, n_tt = (a.T + RT_TOKS - 1) / RT_TOKS;
+        const int rows = a.T <= BIV_RT_RB4_T ? 8 : 16;
+        const int n_tr = (a.n_expert + 1 + rows - 1) / rows, n_tt = (a.T + RT_TOKS - 1) / RT_TOKS;
         const int qblocks = a.T * (a.E / 32), nq = (qblocks + 4 * 256 - 1) / (4 * 256);
-        k_router_tiled<<<n_tr * n_tt + nq, 256, 0, st>>>(a, n_tr, n_tt);
+        if (rows == 8) k_router_tiled<4><<<n_tr * n_tt + nq, 256, 0, st>>>(a, n_tr, n_tt);
+        else k_router_tiled<8><<<n_tr * n_tt + nq, 256, 0, st>>>(a, n_tr, n_tt);
         return hipGetLastError();
     }
     const int rows = a.n_expert + 1;
