@@ -700,8 +700,11 @@ __global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
 #pragma unroll
                     for (int jr = 0; jr < AJ; jr++) dxs[jr] = dxr[jr];
                     // the A words: low halves under one exec mask, high halves
-                    // under the other, exec restored, then a wait for them
+                    // under the other, exec restored, then a wait for them.
+                    // The control flow here is uniform (every lane active),
+                    // so the masks only narrow exec for the reads.
                     constexpr int PO = 2 * XRS * 8; // bytes from pair to pair
+                    static_assert(PO * (NPR - 1) + 128 < 65536, "ds_read offsets are 16-bit");
                     uint64_t ex;
                     if constexpr (AJ == 1) {
                         asm volatile("s_mov_b64 %0, exec\n\ts_mov_b64 exec, %3\n\t"
