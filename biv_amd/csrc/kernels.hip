@@ -1998,7 +1998,7 @@ template <int TY, bool GATEUP>
 hipError_t launch_long_x(const LongArgs &a, hipStream_t st)
 {
     // tokens per workgroup: as few accumulators as the batch needs
-    const int xt = a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : LXT;
+    const int xt = a.T <= 1 ? 1 : a.T <= 2 ? 2 : a.T <= 4 ? 4 : a.T == 5 ? 5 : LXT;
     // every chunk of a workgroup's rows in LDS when that fits (the weights
     // then stream LPD chunks ahead), else two chunks at a time
     const size_t piece_row = TY == T_BF16 ? LK / 4 : LK / 16 + LK / 128;
@@ -2008,6 +2008,7 @@ hipError_t launch_long_x(const LongArgs &a, hipStream_t st)
     case 1: return launch_long_t<TY, GATEUP, 1>(a, full, full_lds, st);
     case 2: return launch_long_t<TY, GATEUP, 2>(a, full, full_lds, st);
     case 4: return launch_long_t<TY, GATEUP, 4>(a, full, full_lds, st);
+    case 5: return launch_long_t<TY, GATEUP, 5>(a, full, full_lds, st);
     default: return launch_long_t<TY, GATEUP, LXT>(a, full, full_lds, st);
     }
 }
