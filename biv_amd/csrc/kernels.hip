@@ -1879,11 +1879,19 @@ hipError_t launch_router(const RouterArgs &a, hipStream_t st)
     // quantisation workgroups beside the row groups: about one block per thread
     const int qblocks = a.T * (a.E / 32);
     // 8 rows per workgroup; tokens split over grid.y in chunks of TC (32 KB of
-    // LDS, 64 KB past 8 tokens)
+    // LDS, 64 KB past 2 TC tokens); batches of 2..64 tokens in chunks of TC / 4
+    // (up to 16 tokens) or TC / 2: more workgroups, shorter chains each
 #define BIV_ROUTER_CASE(NS)                                                                                     \
     if (a.E == 32 * NS) {                                                                                       \
         constexpr int TC = 8192 / (32 * NS);                                                                    \
-        if (a.T <= 2 * TC) {                                                                                    \
+        if (a.T > 1 && a.T <= 64) {                                                                             \
+            /* small batches: one or two tokens per workgroup, more workgroups */                               \
+            constexpr int TS1 = TC / 4 > 0 ? TC / 4 : 1, TS2 = TC / 2 > 0 ? TC / 2 : 1;                         \
+            const int ts = a.T <= 16 ? TS1 : TS2, gy = (a.T + ts - 1) / ts;                                     \
+            const dim3 grid((rows + 7) / 8 + (qblocks + 256 * gy - 1) / (256 * gy), gy);                        \
+            if (ts == TS1) k_router<NS, TS1><<<grid, 256, 0, st>>>(a);                                          \
+            else k_router<NS, TS2><<<grid, 256, 0, st>>>(a);                                                    \
+        } else if (a.T <= 2 * TC) {                                                                             \
             const int gy = (a.T + TC - 1) / TC;                                                                 \
             k_router<NS, TC><<<dim3((rows + 7) / 8 + (qblocks + 256 * gy - 1) / (256 * gy), gy), 256, 0, st>>>(a); \
         } else {                                                                                                \
