@@ -144,15 +144,16 @@ __device__ inline void load32(const float *p, float (&v)[32])
 //
 // A workgroup holds 8 rows in registers and meets TC tokens, staged in LDS;
 // tokens go two at a time, two independent chains per lane.
-template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(RouterArgs a)
+template <int NS, int TC, int NTH = 256> __global__ __launch_bounds__(NTH) void k_router(RouterArgs a)
 {
+    constexpr int RPW = NTH / 32; // rows per workgroup (a half wave each)
     constexpr int E = 32 * NS;
     const float *__restrict__ router = a.router;
     const float *__restrict__ h = a.h;
     const int n_expert = a.n_expert, T = a.T;
     // Workgroups past the row groups quantise h for the experts (Q8 rows in
     // the chain layout): one 32-element block per thread and turn.
-    const int n_rw = (n_expert + 1 + 7) / 8;
+    const int n_rw = (n_expert + 1 + RPW - 1) / RPW;
     if ((int)blockIdx.x >= n_rw) {
         const int nq = gridDim.x - n_rw, nthreads = nq * gridDim.y * blockDim.x;
         for (int i = ((blockIdx.x - n_rw) * gridDim.y + blockIdx.y) * blockDim.x + threadIdx.x; i < T * (E / 32);
@@ -185,14 +186,14 @@ template <int NS, int TC> __global__ __launch_bounds__(256) void k_router(Router
     __shared__ float xs[TC][E];
     const int t0 = blockIdx.y * TC, nt = min(TC, T - t0);
     {
-        constexpr int NP = TC * (E / 4) / 256; // 16-byte pieces per thread
+        constexpr int NP = TC * (E / 4) / NTH; // 16-byte pieces per thread
         const float4 *src = reinterpret_cast<const float4 *>(h + (size_t)t0 * E);
         float4 *dst = reinterpret_cast<float4 *>(&xs[0][0]) + (threadIdx.x & ~(WAVE - 1));
 #pragma unroll
         for (int c = 0; c < NP; c++) {
-            if (c * 256 >= nt * (E / 4)) break; // uniform
-            const int idx0 = c * 256 + (int)threadIdx.x, idx = idx0 < nt * (E / 4) ? idx0 : nt * (E / 4) - 1;
-            __builtin_amdgcn_global_load_lds(src + idx, (__attribute__((address_space(3))) void *)(dst + c * 256), 16, 0,
+            if (c * NTH >= nt * (E / 4)) break; // uniform
+            const int idx0 = c * NTH + (int)threadIdx.x, idx = idx0 < nt * (E / 4) ? idx0 : nt * (E / 4) - 1;
+            __builtin_amdgcn_global_load_lds(src + idx, (__attribute__((address_space(3))) void *)(dst + c * NTH), 16, 0,
                                              0);
         }
     }
@@ -1865,6 +1866,10 @@ hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, i
     return hipGetLastError();
 }
 
+// threads of a router workgroup for a single token (two rows each)
+#ifndef BIV_ROUTER_T1_NTH
+#define BIV_ROUTER_T1_NTH 64
+#endif
 hipError_t launch_router(const RouterArgs &a, hipStream_t st)
 {
     if (a.T >= RT_MIN_T && a.E % (32 * RT_KC) == 0) {
@@ -1891,6 +1896,9 @@ hipError_t launch_router(const RouterArgs &a, hipStream_t st)
             const dim3 grid((rows + 7) / 8 + (qblocks + 256 * gy - 1) / (256 * gy), gy);                        \
             if (ts == TS1) k_router<NS, TS1><<<grid, 256, 0, st>>>(a);                                          \
             else k_router<NS, TS2><<<grid, 256, 0, st>>>(a);                                                    \
+        } else if (a.T == 1 && BIV_ROUTER_T1_NTH != 256) {                                                      \
+            constexpr int N1 = BIV_ROUTER_T1_NTH;                                                               \
+            k_router<NS, TC, N1><<<dim3((rows + N1 / 32 - 1) / (N1 / 32) + (qblocks + N1 - 1) / N1, 1), N1, 0, st>>>(a); \
         } else if (a.T <= 2 * TC) {                                                                             \
             const int gy = (a.T + TC - 1) / TC;                                                                 \
             k_router<NS, TC><<<dim3((rows + 7) / 8 + (qblocks + 256 * gy - 1) / (256 * gy), gy), 256, 0, st>>>(a); \
