@@ -305,6 +305,19 @@ def test_bf16_full_size_4096(orc, engine):
     _full_size(orc, moe, layer, synth.make_tokens(4096, 4096))
 
 
+@pytest.mark.parametrize("T", [1, 5, 64, 300])
+def test_other_widths(orc, engine, T):
+    """A layer of other widths: n_embd 1024, n_ff 1024, 64 experts (the
+    K = 1024 instances of every kernel, the router's 32-step rows)."""
+    print(f"case widths 1024 T={T}", flush=True)
+    layer, moe = layer_for(engine, seed=41, n_embd=1024, n_ff=1024, n_ff_sh=1024, n_expert=64)
+    h = synth.make_tokens(500 + T, T, n_embd=1024, offsets=T > 1)
+    if T < 64:
+        full_parity(orc, engine, layer, moe, h, block_dots=T == 5)
+    else:
+        _full_size(orc, moe, layer, h)
+
+
 def test_mixed_shared_types_prefill(orc, engine):
     """Q4_K routed and Q8_0 shared gate/up at T = 70: two matrix-core launches."""
     print("case mixed shared prefill", flush=True)
