@@ -580,9 +580,12 @@ template <int TY, int K, bool DUMP>
 #define GU_EXACT_AJ 2 // blocks per LDS read group, Q8_0
 #endif
 #ifndef GU_EXACT_AJ_Q4K
-#define GU_EXACT_AJ_Q4K 1 // and Q4_K (fewer registers)
+#define GU_EXACT_AJ_Q4K 2 // and Q4_K
 #endif
-__global__ __launch_bounds__(QNTH) void k_gu_exact(MvArgs a)
+// four waves per SIMD (two workgroups per CU, as the LDS allows): the
+// registers are held to 128 (Q4_K then spills 6 of them to scratch, still
+// faster than three waves per SIMD without spills)
+__global__ __launch_bounds__(QNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 : 4))) void k_gu_exact(MvArgs a)
 {
     using W = GuW<TY, K>;
     constexpr int NB = K / 32;
