@@ -364,14 +364,23 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float *x, float *y, cons
     // the chain); NPL = 0: any n (a multiple of 32), read twice
     const int L = threadIdx.x & 31;
     const int row = blockIdx.x * (blockDim.x / 32) + (threadIdx.x >> 5);
-    if (row >= rows) return; // uniform over the half wave; no shuffles cross halves
     const float *g = x + (size_t)row * n;
     float *o = y + (size_t)row * n;
     float acc = 0.0f;
     float gv[NPL > 0 ? NPL : 1];
+    // NPL > 0: the norm weights staged in LDS once per workgroup, read
+    // after the chain (a short LDS latency rather than an L2 one)
+    __shared__ float wl[NPL > 0 ? 32 * NPL : 1];
     if constexpr (NPL > 0) {
+        if (row < rows) {
 #pragma unroll
-        for (int k = 0; k < NPL; k++) gv[k] = g[L + 32 * k];
+            for (int k = 0; k < NPL; k++) gv[k] = g[L + 32 * k];
+        }
+        for (int i = threadIdx.x; i < 32 * NPL; i += blockDim.x) wl[i] = w[i];
+        __syncthreads();
+    }
+    if (row >= rows) return; // uniform over the half wave; no shuffles cross halves
+    if constexpr (NPL > 0) {
 #pragma unroll
         for (int k = 0; k < NPL; k++) acc = fmaf(gv[k], gv[k], acc);
     } else {
@@ -387,7 +396,7 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float *x, float *y, cons
     const float scale = 1.0f / sqrtf(ss + eps);
     if constexpr (NPL > 0) {
 #pragma unroll
-        for (int k = 0; k < NPL; k++) o[L + 32 * k] = gv[k] * (scale * w[L + 32 * k]);
+        for (int k = 0; k < NPL; k++) o[L + 32 * k] = gv[k] * (scale * wl[L + 32 * k]);
     } else {
         for (int i = L; i < n; i += 32) o[i] = g[i] * (scale * w[i]);
     }
