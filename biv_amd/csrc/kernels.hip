@@ -749,21 +749,42 @@ __device__ void route_block_counts(const int *ids, int n_expert, int k, int T, i
     for (int e = threadIdx.x; e < MAX_EXPERTS; e += blockDim.x) work[(size_t)b * MAX_EXPERTS + e] = __popc(mask[e]);
 }
 
-__global__ __launch_bounds__(MAX_EXPERTS) void k_dispatch_scan(int n_expert, int nb, int chunk, Dispatch dp, int *work)
+constexpr int DS_SPLIT = 4; // threads per expert column in k_dispatch_scan
+__global__ __launch_bounds__(MAX_EXPERTS *DS_SPLIT) void k_dispatch_scan(int n_expert, int nb, int chunk, Dispatch dp,
+                                                                         int *work)
 {
-    const int e = threadIdx.x, lane = e & (WAVE - 1), w = e >> 6;
-    // the column of block counts, 16 loads in flight at a time
-    int run = 0;
-    for (int b0 = 0; b0 < nb; b0 += 16) {
+    // DS_SPLIT threads per expert, each over a run of the blocks: its sum,
+    // the runs' offsets, then its blocks' exclusive prefixes (16 loads in
+    // flight at a time; integer sums, so the result does not depend on the
+    // split)
+    const int e = threadIdx.x & (MAX_EXPERTS - 1), qs = threadIdx.x / MAX_EXPERTS;
+    const int lane = e & (WAVE - 1), w = e >> 6;
+    const int nbq = (nb + DS_SPLIT - 1) / DS_SPLIT, b_lo = min(nb, qs * nbq), b_hi = min(nb, b_lo + nbq);
+    __shared__ int part[DS_SPLIT][MAX_EXPERTS];
+    int sum = 0;
+    for (int b0 = b_lo; b0 < b_hi; b0 += 16) {
         int v[16];
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = b0 + j < nb ? work[(size_t)(b0 + j) * MAX_EXPERTS + e] : 0;
+        for (int j = 0; j < 16; j++) v[j] = b0 + j < b_hi ? work[(size_t)(b0 + j) * MAX_EXPERTS + e] : 0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) sum += v[j];
+    }
+    part[qs][e] = sum;
+    __syncthreads();
+    int run = 0;
+    for (int i = 0; i < qs; i++) run += part[i][e];
+    for (int b0 = b_lo; b0 < b_hi; b0 += 16) {
+        int v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = b0 + j < b_hi ? work[(size_t)(b0 + j) * MAX_EXPERTS + e] : 0;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            if (b0 + j < nb) work[(size_t)(b0 + j) * MAX_EXPERTS + e] = run;
+            if (b0 + j < b_hi) work[(size_t)(b0 + j) * MAX_EXPERTS + e] = run;
             run += v[j];
         }
     }
+    run = 0;
+    for (int i = 0; i < DS_SPLIT; i++) run += part[i][e];
     const int tot = e < n_expert ? run : 0, nsl = (tot + chunk - 1) / chunk;
     // exclusive scans over the experts of the pair and slot totals
     __shared__ int wsum[2][MAX_EXPERTS / WAVE];
@@ -776,11 +797,12 @@ __global__ __launch_bounds__(MAX_EXPERTS) void k_dispatch_scan(int n_expert, int
             y += ys;
         }
     }
-    if (lane == WAVE - 1) {
+    if (lane == WAVE - 1 && qs == 0) {
         wsum[0][w] = x;
         wsum[1][w] = y;
     }
     __syncthreads();
+    if (qs != 0) return; // the experts' scans and records: one thread per expert
     int px = 0, py = 0;
     for (int i = 0; i < w; i++) {
         px += wsum[0][i];
@@ -1932,7 +1954,7 @@ hipError_t launch_route_sort(const float *logits, int n_expert, int k, int T, in
     const int threads = groups == 1 ? WAVE * T : RS_THREADS; // a wavefront per token
     k_route_sort<<<groups, threads, 0, st>>>(logits, n_expert, k, T, chunk, dp, work);
     if (groups > 1) {
-        k_dispatch_scan<<<1, MAX_EXPERTS, 0, st>>>(n_expert, groups, chunk, dp, work);
+        k_dispatch_scan<<<1, MAX_EXPERTS * DS_SPLIT, 0, st>>>(n_expert, groups, chunk, dp, work);
         k_dispatch_place<<<groups, 256, 0, st>>>(n_expert, k, T, groups, chunk, dp, work);
     }
     return hipGetLastError();
