@@ -570,6 +570,14 @@ void orc_rms_norm(float *x, const float *w, size_t rows, size_t n, float eps, in
     }
 }
 
+/* The integer whose signed order is f32::total_cmp's order of x. */
+static int32_t total_key(float x)
+{
+    int32_t b;
+    memcpy(&b, &x, sizeof b);
+    return b ^ (int32_t)((uint32_t)(b >> 31) >> 1);
+}
+
 /* model.rs:256-268: softmax, then the k highest probabilities (the lower
  * index first among equals), weighted by p / max(sum of the k, 1/16384). */
 void orc_route(const float *logits, size_t ne, size_t k, int32_t *ids, float *w)
@@ -578,12 +586,14 @@ void orc_route(const float *logits, size_t ne, size_t k, int32_t *ids, float *w)
     unsigned char *taken = calloc(ne, 1);
     memcpy(p, logits, sizeof(float) * ne);
     orc_softmax(p, ne);
-    /* selection by repeated maximum is the first k of the stable sort */
+    /* selection by repeated maximum is the first k of the stable sort; the
+     * comparison is f32::total_cmp's (model.rs:264): the bits as a signed
+     * magnitude, so +NaN ranks above +inf and -NaN below -inf */
     for (size_t j = 0; j < k; j++) {
         size_t best = ne;
         for (size_t i = 0; i < ne; i++) {
             if (taken[i]) continue;
-            if (best == ne || p[i] > p[best]) best = i;
+            if (best == ne || total_key(p[i]) > total_key(p[best])) best = i;
         }
         taken[best] = 1;
         ids[j] = (int32_t)best;

@@ -277,3 +277,147 @@ def test_moe_shared_expert_gate(orc):
     g = h @ gi.data.view(np.float32).astype(np.float64)
     want = routed + (1 / (1 + np.exp(-g)))[:, None] * ys
     assert np.allclose(out, want, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# float64 brute force of the composite functions: rms_norm, the SwiGLU of
+# dense_ffn and the weighted combine of the MoE block.  Each expected value is
+# built from dequantize_row and q8act only (both pinned above), never from the
+# oracle function under test, and each test also shows that a plausible
+# mistake (a swapped operand, a dropped term) lands far outside its bar.
+
+def _deq(orc, ty, data, rows, cols):
+    rs = orc.row_size(ty, cols)
+    return np.stack([orc.dequantize_row(ty, data[r * rs:(r + 1) * rs], cols) for r in range(rows)]).astype(np.float64)
+
+
+def _q8_f64(orc, x):
+    """The Q8 activations of each row of x as float64 values qs * d."""
+    x = np.atleast_2d(np.asarray(x, np.float32))
+    out = np.empty(x.shape, np.float64)
+    for i, row in enumerate(x):
+        qs, d, _ = orc.q8act(row)
+        out[i] = qs.astype(np.float64) * np.repeat(d.astype(np.float64), 32)
+    return out
+
+
+def _silu64(g):
+    return g / (1.0 + np.exp(-g))
+
+
+def _dense64(orc, Wg, Wu, Wd, x, swap=False):
+    """down . q8(silu(gate . q8(x)) * (up . q8(x))) in float64 (model.rs:1118-1126)."""
+    xq = _q8_f64(orc, x)
+    g, u = xq @ Wg.T, xq @ Wu.T
+    if swap:
+        g, u = u, g
+    a = _silu64(g) * u
+    return _q8_f64(orc, a.astype(np.float32)) @ Wd.T
+
+
+def _rel(a, b):
+    return float(np.abs(np.asarray(a, np.float64) - b).max() / np.sqrt(np.mean(np.asarray(b, np.float64) ** 2)))
+
+
+@pytest.mark.parametrize("eps", [1e-6, 0.5])
+def test_rms_norm_float64(orc, eps):
+    """ops::rms_norm (ops.rs:136-144): x / sqrt(mean(x^2) + eps) * w per row.
+    eps = 0.5 on rows of small values makes a dropped or misplaced eps, a sum
+    instead of a mean, or a missing sqrt fail."""
+    rng = np.random.default_rng(21)
+    n = 2048
+    w = (1 + 0.5 * rng.standard_normal(n)).astype(np.float32)
+    x = (rng.standard_normal((7, n)) * (0.3 if eps > 0.1 else 2.0)).astype(np.float32)
+    x[3] = 0.0  # zero row: scale 1/sqrt(eps), output 0
+    got = orc.rms_norm(x, w, eps)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt(np.mean(x64 ** 2, axis=1, keepdims=True) + eps) * w.astype(np.float64)
+    # a few f32 roundings per element: ss, the division, sqrt, 1/., scale*w, v*.
+    assert np.all(np.abs(got - want) <= 8 * np.finfo(np.float32).eps * np.abs(want) + 1e-30)
+    assert not np.any(got[3])
+    if eps > 0.1:
+        nz = np.arange(7) != 3
+        wrong = x64[nz] / np.sqrt(np.mean(x64[nz] ** 2, axis=1, keepdims=True)) * w  # eps dropped
+        assert np.abs(wrong - want[nz]).max() > 1e-2 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("types", [(Q8_0, Q8_0, Q8_0), (Q4K, Q4K, Q6K)])
+def test_dense_ffn_float64(orc, types):
+    """dense_ffn (model.rs:1118-1126): down . q8(silu(gate . x) * (up . x))
+    with gate and up different matrices.  Against float64 sums of the
+    dequantised rows; the bar is a few re-quantisation steps of the
+    intermediate (a value near a rounding boundary can land on either side),
+    while silu on the wrong matrix misses it by two orders of magnitude."""
+    from biv_amd import synth
+    rng = np.random.default_rng(33)
+    e, ff, n = 512, 256, 6
+    gty, uty, dty = types
+    gw, uw, dw = (synth.make_weight(rng, gty, e, ff), synth.make_weight(rng, uty, e, ff),
+                  synth.make_weight(rng, dty, ff, e))
+    x = rng.standard_normal((n, e)).astype(np.float32)
+    got = orc.dense_ffn(gty, gw.data, uty, uw.data, dty, dw.data, e, ff, x)
+    Wg, Wu, Wd = _deq(orc, gty, gw.data, ff, e), _deq(orc, uty, uw.data, ff, e), _deq(orc, dty, dw.data, e, ff)
+    want = _dense64(orc, Wg, Wu, Wd, x)
+    assert _rel(got, want) < 5e-4
+    assert _rel(_dense64(orc, Wg, Wu, Wd, x, swap=True), want) > 0.3
+
+
+def test_moe_k3_weighted_combine_float64(orc):
+    """Model::moe (model.rs:860-898) with k = 3 distinct weights per token and
+    a shared expert: out_t = sum_j w_j * y_{e_j}(h_t) + sigmoid(gate_inp . h_t)
+    * y_shared(h_t), with route (model.rs:256-268) redone in float64 (softmax,
+    the three highest, p / their sum) and every expert's SwiGLU in float64."""
+    from biv_amd import synth
+    e, ne, k, ff = 256, 8, 3, 64
+    layer = synth.make_layer(41, n_embd=e, n_expert=ne, k=k, n_ff=ff, n_ff_sh=ff)
+    h = synth.make_tokens(42, 5, e)
+    out, ids, w, _ = orc.moe(layer, h, taps=True)
+    R = layer.router.data.view(np.float32).reshape(ne, e).astype(np.float64)
+    h64 = h.astype(np.float64)
+    logits = h64 @ R.T
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    want_ids = np.argsort(-p, axis=1, kind="stable")[:, :k]
+    assert np.array_equal(ids, want_ids)
+    want_w = np.take_along_axis(p, want_ids, 1)
+    want_w /= want_w.sum(axis=1, keepdims=True)
+    assert np.allclose(w, want_w, rtol=1e-5)
+    assert all(len(set(np.round(r, 6))) == k for r in want_w), "weights must be distinct to pin the combine"
+    ys = []
+    for x_ in range(ne):
+        Wg = _deq(orc, Q8_0, layer.gate.expert(x_), ff, e)
+        Wu = _deq(orc, Q8_0, layer.up.expert(x_), ff, e)
+        Wd = _deq(orc, Q8_0, layer.down.expert(x_), e, ff)
+        ys.append(_dense64(orc, Wg, Wu, Wd, h))
+    sg, su, sd, gi = layer.shared
+    ysh = _dense64(orc, _deq(orc, Q8_0, sg.data, ff, e), _deq(orc, Q8_0, su.data, ff, e),
+                   _deq(orc, Q8_0, sd.data, e, ff), h)
+    gate = 1 / (1 + np.exp(-(h64 @ gi.data.view(np.float32).astype(np.float64))))
+    want = np.zeros((h.shape[0], e))
+    for t in range(h.shape[0]):
+        for j in range(k):
+            want[t] += want_w[t, j] * ys[want_ids[t, j]][t]
+        want[t] += gate[t] * ysh[t]
+    assert _rel(out, want) < 5e-4
+    # weights applied in the wrong rank order, or the shared gate dropped, miss the bar
+    bad = np.zeros_like(want)
+    for t in range(h.shape[0]):
+        for j in range(k):
+            bad[t] += want_w[t, k - 1 - j] * ys[want_ids[t, j]][t]
+        bad[t] += gate[t] * ysh[t]
+    assert _rel(bad, want) > 2e-2
+    assert _rel(want - gate[:, None] * ysh, want) > 2e-2
+
+
+def test_route_total_order_nan(orc):
+    """route sorts with f32::total_cmp (model.rs:264): +NaN ranks above every
+    number and -NaN below.  Logits [-NaN, 1, 2, +NaN]: softmax's max ignores
+    NaN (f32::max); the index-order sum takes the first NaN it meets (-NaN) and
+    x86 NaN propagation gives p = [-NaN, -NaN, -NaN, +NaN].  So the top 3 are
+    expert 3, then 0 and 1 (equal keys, lower index first)."""
+    l = np.array([0, 1.0, 2.0, 0], np.float32)
+    l.view(np.uint32)[0] = 0xFFC00000
+    l.view(np.uint32)[3] = 0x7FC00000
+    ids, w = orc.route(l, 3)
+    assert list(ids) == [3, 0, 1]
+    assert np.all(np.isnan(w))
