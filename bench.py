@@ -97,6 +97,15 @@ def bench_gpu(eng, moes, layer, T, steps, warmup, torch):
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall
     ms = t0.elapsed_time(t1) / steps
+    # per-step distribution: an event between consecutive steps (the launches
+    # queue ahead, so each interval is one step's time on the GPU)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    evs[0].record()
+    for i in range(steps):
+        moes[i % L].forward_device(h_dev.data_ptr(), T, out_dev.data_ptr())
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    per = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]) * 1e3
     # a second timed region with an event around every stage, for the
     # per-kernel roofline (events add small gaps, so not the headline)
     eng.set_timing(True)
@@ -109,9 +118,13 @@ def bench_gpu(eng, moes, layer, T, steps, warmup, torch):
     res = {
         "T": T, "U": U, "us_per_layer": round(ms * 1e3, 3), "tokens_per_s": round(T / (ms * 1e-3), 1),
         "layer_GBps": round(B / (ms * 1e-3) / 1e9, 1), "layer_hbm_frac": round(B / (ms * 1e-3) / HBM_PEAK, 4),
+        "us_median": round(float(np.median(per)), 3), "us_p10": round(float(np.percentile(per, 10)), 3),
+        "us_p90": round(float(np.percentile(per, 90)), 3),
         "stage_us": {k: round(v, 3) for k, v in stage_us.items()},
         "wall_s": round(wall, 3),
     }
+    if T >= 64:
+        res["mfma"] = mfma_block(T, ms)
     # the dominant kernel alone: launched back to back over the layer copies
     # (the stage events above add a dispatch gap to every stage)
     dom = max(("gate_up", "down", "router"), key=lambda s: stage_us[s])
@@ -122,6 +135,60 @@ def bench_gpu(eng, moes, layer, T, steps, warmup, torch):
                        "unit": "GB/s", "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": TRAFFIC.get((dom, T)),
                        "bytes_per_launch": dbytes, "avg_us": round(kern_us, 3)}
     return res
+
+
+OPS_PER_TOKEN = (K + 1) * 3 * 2 * E * FF   # int8 ops of the routed pairs and the shared row: 56,623,104
+INT8_PEAK = 5.0e15
+
+
+def mfma_block(T, ms, bytes_=None):
+    """Algorithmic int8 ops of the layer per second against the dense int8
+    MFMA peak, and the cap the HBM roofline puts on it at this arithmetic
+    intensity (ops per algorithmic byte x 8 TB/s)."""
+    ops = OPS_PER_TOKEN * T
+    ach = ops / (ms * 1e-3)
+    res = {"achieved": round(ach / 1e12, 2), "peak": INT8_PEAK / 1e12, "unit": "TOP/s",
+           "frac": round(ach / INT8_PEAK, 5)}
+    if bytes_ is None:
+        bytes_ = layer_bytes(NE, T)
+    cap = min(INT8_PEAK, ops / bytes_ * HBM_PEAK)
+    res["hbm_cap"] = round(cap / 1e12, 1)
+    res["frac_of_cap"] = round(ach / cap, 4)
+    return res
+
+
+def bench_graph_chain(eng, moes, layer, T, reps, torch):
+    """The decode step as a serving loop runs it: the L layer copies' forwards
+    captured into one HIP graph and replayed (a chain of L layers at T = 1),
+    reported as total / L.  Each replay is checked against the eager
+    result of the last layer."""
+    L = len(moes)
+    h_dev = torch.from_numpy(tokens_for(layer, T, 1000 + T)).cuda()
+    out_dev = torch.empty_like(h_dev)
+    for m in moes:
+        m.forward_device(h_dev.data_ptr(), T, out_dev.data_ptr())
+    torch.cuda.synchronize()
+    want = out_dev.clone()
+    stream = torch.cuda.current_stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for m in moes:
+            m.forward_device(h_dev.data_ptr(), T, out_dev.data_ptr())
+    ok = True
+    for _ in range(3):
+        out_dev.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        ok &= bool(torch.equal(out_dev, want))
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / (reps * L)
+    return {"T": T, "layers_in_graph": L, "replays": reps, "us_per_layer": round(ms * 1e3, 3),
+            "tokens_per_s": round(T / (ms * 1e-3), 1), "replays_match_eager": ok}
 
 
 def bench_config(eng, layer, copies, T, steps, warmup, torch):
@@ -142,8 +209,13 @@ def bench_config(eng, layer, copies, T, steps, warmup, torch):
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
-    return {"T": T, "us_per_layer": round(ms * 1e3, 3), "tokens_per_s": round(T / (ms * 1e-3), 1),
-            "layers_rotated": copies}
+    res = {"T": T, "us_per_layer": round(ms * 1e3, 3), "tokens_per_s": round(T / (ms * 1e-3), 1),
+           "layers_rotated": copies}
+    if T >= 64:
+        # Q4_K gate/up (144 B per 256) and Q6_K down (210 B per 256): 2,039,808 B per expert
+        ebytes = 2 * FF * (E // 256 * 144) + E * (FF // 256 * 210)
+        res["mfma"] = mfma_block(T, ms, (NE + 1) * ebytes + ROUTER_BYTES + 2 * T * E * 4)
+    return res
 
 
 def bench_bf16_stack(eng, T, n_layers, passes, torch):
@@ -233,7 +305,8 @@ def bench_cpu(layer, T, seconds):
     import oracle
     if not os.path.exists(oracle.LIB_PATH):
         oracle.build()
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
+    # every core this process may run on (the box's share of the host)
+    threads = len(os.sched_getaffinity(0))
     h = tokens_for(layer, T, 1000 + T)
     oracle.moe(layer, h, threads=threads)  # warm
     n, t0 = 0, time.perf_counter()
@@ -242,7 +315,8 @@ def bench_cpu(layer, T, seconds):
         n += 1
     dt = (time.perf_counter() - t0) / n
     level = {0: "scalar", 1: "avx2", 2: "avxvnni"}[oracle.detect_level()]
-    return {"value": round(T / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": round(T / dt, 2), "unit": "tokens/s", "cores": threads, "host_cpus": os.cpu_count(),
+            "kind": "port",
             "us_per_layer": round(dt * 1e6, 1), "kernels": level,
             "sample": f"{n} forwards of the same T={T} Q8_0 layer ({seconds:.0f} s budget)"}
 
@@ -260,6 +334,8 @@ def main():
                     help="other BASELINE configs to run: kquant (Q4_K/Q6_K at T=1, 2048), bf16 (the 40-layer BF16 "
                          "stack at T=4096), dense (the qwen35 dense FFN, 4096 x 12288 Q8_0); '' for none")
     ap.add_argument("--bf16-layers", type=int, default=40)
+    ap.add_argument("--graph-reps", type=int, default=50,
+                    help="replays of the graph-captured chain of --layers layers at T=1 (0 to skip)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (a kernel of known traffic, to scale "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counts)")
@@ -295,6 +371,12 @@ def main():
         steps = args.steps if T <= 64 else max(20, args.steps // 4)
         sweep[str(T)] = bench_gpu(eng, moes, layer, T, steps, args.warmup, torch)
         log(f"T={T}: {sweep[str(T)]}")
+
+    if args.graph_reps > 0:
+        graph = bench_graph_chain(eng, moes, layer, 1, args.graph_reps, torch)
+        log(f"graph chain T=1: {graph}")
+    else:
+        graph = None
 
     extra = {}
     todo = {c.strip() for c in args.configs.split(",") if c.strip()}
@@ -339,6 +421,7 @@ def main():
         "stage_us": main_res["stage_us"],
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "graph_chain_T1": graph,
         "configs": extra,
     }
     print(json.dumps(line), flush=True)
