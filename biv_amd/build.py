@@ -39,8 +39,7 @@ def build(verbose=False, defines=(), out=OUT):
     none."""
     objdir = os.path.join(HERE, "_build" if not defines else "_build_" + "_".join(defines).replace("=", ""))
     os.makedirs(objdir, exist_ok=True)
-    objs = []
-    for src in SOURCES:
+    def compile_one(src):
         obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
         lang = ["-x", "hip"]
         cmd = [hipcc()] + FLAGS + ["-D" + d for d in defines] + lang + ["-I", os.path.join(ROOT, "include"), "-c", os.path.join(CSRC, src), "-o", obj]
@@ -53,7 +52,12 @@ def build(verbose=False, defines=(), out=OUT):
             raise RuntimeError(f"hipcc failed on {src}:\n{err}")
         if err.strip() and verbose:
             print(err)
-        objs.append(obj)
+        return obj
+
+    # the sources compile independently: one hipcc each, side by side
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+        objs = list(ex.map(compile_one, SOURCES))
     cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", out] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

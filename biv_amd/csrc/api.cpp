@@ -6,6 +6,7 @@
 #include "layout.hpp"
 
 #include <algorithm>
+#include <new>
 #include <cstdlib>
 #include <cstdarg>
 #include <cstdio>
@@ -156,8 +157,25 @@ int dev_alloc(biv_hip_ctx *ctx, size_t bytes, uint8_t **out)
 
 // Repack n matrices of rows x cols from ggml rows (matrix e at
 // data + e*stride + offset) into the planes of DevMat.
+int upload_mat_impl(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, const uint8_t *data, size_t stride,
+                    size_t offset, DevMat &m);
+
+// upload_mat_impl with host allocation failures (its repacking buffers)
+// turned into an error code rather than an exception through the C ABI
 int upload_mat(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, const uint8_t *data, size_t stride,
                size_t offset, DevMat &m)
+{
+    if (cols > INT32_MAX || rows > INT32_MAX || n > INT32_MAX)
+        return fail(ctx, BIV_HIP_E_INVALID, "shape %zux%zux%zu out of range", cols, rows, n);
+    try {
+        return upload_mat_impl(ctx, ty, cols, rows, n, data, stride, offset, m);
+    } catch (const std::bad_alloc &) {
+        return fail(ctx, BIV_HIP_E_NOMEM, "host memory for repacking %zux%zux%zu", cols, rows, n);
+    }
+}
+
+int upload_mat_impl(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n, const uint8_t *data, size_t stride,
+                    size_t offset, DevMat &m)
 {
     size_t be, bb;
     if (!block_of(ty, be, bb)) return fail(ctx, BIV_HIP_E_TYPE, "no kernel for ggml type %d", ty);
@@ -457,8 +475,11 @@ struct StageMarks {
 // Queue the whole block: h and out are device pointers.  With only >= 0,
 // queue stage `only` alone (for measurement: the scratch holds a forward's
 // routing of the same T).
+// With norm_w, h is the residual x and the block takes rms_norm(x) with
+// these weights (the post_norm of model.rs:786-790), formed by the router
+// launch into the scratch row block h_stage.
 int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float *out, unsigned flags,
-            const Dumps &dm, int only = -1)
+            const Dumps &dm, int only = -1, const float *norm_w = nullptr, float eps = 0.0f)
 {
     if (T == 0) return 0;
     int rc = scratch_fit(ctx, m, T);
@@ -503,6 +524,13 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     ra.xq = s.xq;
     ra.xd = s.xd;
     ra.xs = s.xs;
+    ra.norm_w = norm_w;
+    ra.eps = eps;
+    ra.hn = s.h_stage;
+    if (norm_w) {
+        if (h == s.h_stage) return fail(ctx, BIV_HIP_E_INVALID, "post_norm input aliases its output");
+        h = s.h_stage; // every later use of h takes the normalised rows
+    }
     MARK();
     if (run(0)) HIP_TRY(ctx, biv::launch_router(ra, st), "router");
     MARK();
@@ -988,9 +1016,7 @@ int biv_hip_moe_ffn_step(biv_hip_ctx *ctx, const biv_hip_moe *moe, float *x_dev,
     if (n == 0) return 0;
     HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
     if ((rc = scratch_fit(ctx, moe, n))) return rc;
-    float *h = ctx->sc.h_stage;
-    HIP_TRY(ctx, biv::launch_rms_norm(x_dev, h, norm_dev, n, moe->E, eps, ctx->stream), "rms_norm");
-    return forward(ctx, moe, h, n, x_dev, BIV_HIP_ADD, Dumps{});
+    return forward(ctx, moe, x_dev, n, x_dev, BIV_HIP_ADD, Dumps{}, -1, norm_dev, eps);
 }
 
 int biv_hip_time_stage(biv_hip_ctx *ctx, const biv_hip_moe *const *moes, int n_moes, const float *h_dev, int n,

@@ -71,6 +71,12 @@ struct RouterArgs {
     float *glogit;         // [T]
     int8_t *xq;            // h quantised: [T][E] chain layout
     float *xd, *xs;        // [T][E/32]
+    // With norm_w: h is the residual x and every use of it takes
+    // rms_norm(x) (ops.rs:136-144) with these weights and eps, the
+    // post_norm before the FFN (model.rs:786-790); hn [T][E] receives it.
+    const float *norm_w;
+    float eps;
+    float *hn;
 };
 // router logits + gate_inp logit + Q8 quantisation of h
 hipError_t launch_router(const RouterArgs &a, hipStream_t st);

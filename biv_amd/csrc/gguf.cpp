@@ -14,6 +14,8 @@
 #include <unistd.h>
 
 #include <cstdarg>
+#include <cstdint>
+#include <new>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -199,8 +201,17 @@ struct biv_gguf {
             t.shard = shard;
             t.offset = c.get<uint64_t>();
             uint64_t ne = 1;
-            for (uint64_t d : t.dims) ne *= d;
-            t.n_bytes = (size_t)(ne / be * bb);
+            for (uint64_t d : t.dims)
+                if (__builtin_mul_overflow(ne, d, &ne))
+                    throw ParseError{BIV_HIP_E_FORMAT, fmt("gguf: tensor %s is too large", t.name.c_str())};
+            if (ne % be)
+                throw ParseError{BIV_HIP_E_FORMAT,
+                                 fmt("gguf: tensor %s has %llu elements, not whole blocks of %zu", t.name.c_str(),
+                                     (unsigned long long)ne, be)};
+            uint64_t nb;
+            if (__builtin_mul_overflow(ne / be, (uint64_t)bb, &nb) || nb > SIZE_MAX)
+                throw ParseError{BIV_HIP_E_FORMAT, fmt("gguf: tensor %s is too large", t.name.c_str())};
+            t.n_bytes = (size_t)nb;
             infos.push_back(std::move(t));
         }
         uint64_t alignment = 32;
@@ -262,6 +273,10 @@ int biv_gguf_open(const char *const *paths, int n_paths, biv_gguf **out)
             g_open_error = e.msg;
             delete g;
             return e.code;
+        } catch (const std::bad_alloc &) {
+            g_open_error = fmt("gguf: out of host memory reading %s", paths[i]);
+            delete g;
+            return BIV_HIP_E_NOMEM;
         }
     }
     *out = g;
@@ -345,6 +360,8 @@ int biv_gguf_read_moe_config(biv_gguf *g, biv_gguf_moe_config *cfg)
     (void)need("expert_shared_feed_forward_length", n_ff_sh);
     g->err.clear();
     if (n_used == 0 || n_used > n_expert) return g->fail(BIV_HIP_E_INVALID, "expert_used_count not in 1..=expert_count");
+    for (uint64_t v : {block_count, n_embd, n_expert, n_ff, n_ff_sh})
+        if (v > INT32_MAX) return g->fail(BIV_HIP_E_INVALID, "a qwen35moe size is out of range");
     if (nextn > block_count) return g->fail(BIV_HIP_E_INVALID, "nextn_predict_layers > block_count");
     float eps = 0.0f;
     if ((rc = biv_gguf_get_f32(g, (arch + ".attention.layer_norm_rms_epsilon").c_str(), &eps))) return rc;
@@ -374,6 +391,8 @@ int biv_gguf_read_dense_config(biv_gguf *g, biv_gguf_dense_config *cfg)
     (void)need("nextn_predict_layers", nextn);
     g->err.clear();
     if (nextn > block_count) return g->fail(BIV_HIP_E_INVALID, "nextn_predict_layers > block_count");
+    for (uint64_t v : {block_count, n_embd, n_ff})
+        if (v > INT32_MAX) return g->fail(BIV_HIP_E_INVALID, "a qwen35 size is out of range");
     float eps = 0.0f;
     if ((rc = biv_gguf_get_f32(g, (arch + ".attention.layer_norm_rms_epsilon").c_str(), &eps))) return rc;
     cfg->n_layer = (int)(block_count - nextn);
@@ -432,6 +451,16 @@ extern "C" int biv_hip_moe_from_gguf(biv_hip_ctx *ctx, biv_gguf *g, int layer, b
     if (layer < 0 || layer >= cfg.n_layer)
         return biv_hip_fail_ext(ctx, BIV_HIP_E_INVALID, fmt("layer %d of %d", layer, cfg.n_layer).c_str());
     const size_t e = cfg.n_embd, n = cfg.n_expert, ff = cfg.n_ff_exp, sff = cfg.n_ff_shexp;
+    // the shapes the kernels take, checked before anything is uploaded
+    // (biv_hip_moe_create checks them again on the uploaded parts)
+    auto width_ok = [](size_t K) { return K == 512 || K == 1024 || K == 2048; };
+    if (!width_ok(e) || !width_ok(ff) || n > 256 || cfg.n_expert_used > 16 || (sff && sff != ff))
+        return biv_hip_fail_ext(ctx, BIV_HIP_E_INVALID,
+                                fmt("n_embd %zu, n_ff %zu, %zu experts (%d used), shared n_ff %zu: the kernels take "
+                                    "n_embd and n_ff of 512, 1024 or 2048, at most 256 experts, k <= 16 and a "
+                                    "shared expert as wide as the routed ones",
+                                    e, ff, n, cfg.n_expert_used, sff)
+                                    .c_str());
     const std::string blk = "blk." + std::to_string(layer) + ".";
     auto find = [&](const std::string &name, std::vector<uint64_t> want, const TensorInfo *&t) -> int {
         t = g->tensor(name + ".weight");

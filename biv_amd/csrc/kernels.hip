@@ -144,6 +144,21 @@ __device__ inline void load32(const float *p, float (&v)[32])
 //
 // A workgroup holds 8 rows in registers and meets TC tokens, staged in LDS;
 // tokens go two at a time, two independent chains per lane.
+// The RMS scale of ops::rms_norm (ops.rs:136-144) of a row of 32 NS floats
+// from the sum of squares of lane L's chain (elements L, L + 32, ...), in
+// every lane of the 32-lane half wave: dot_f32's tree, / n, 1 / sqrt(. + eps).
+__device__ inline float rms_scale(float acc, int n, float eps)
+{
+    float v = acc;
+    v = v + __shfl_xor(v, 8);  // acc0+acc1 (lanes 0-7), acc2+acc3 (16-23)
+    v = v + __shfl_xor(v, 16); // (acc0+acc1)+(acc2+acc3)
+    v = v + __shfl_xor(v, 4);  // the two 128-bit halves
+    v = v + __shfl_xor(v, 2);  // movehl
+    v = v + __shfl_xor(v, 1);  // movehdup
+    const float ss = v / (float)n;
+    return 1.0f / sqrtf(ss + eps);
+}
+
 template <int NS, int TC, int NTH = 256> __global__ __launch_bounds__(NTH) void k_router(RouterArgs a)
 {
     constexpr int RPW = NTH / 32; // rows per workgroup (a half wave each)
@@ -154,6 +169,41 @@ template <int NS, int TC, int NTH = 256> __global__ __launch_bounds__(NTH) void 
     // Workgroups past the row groups quantise h for the experts (Q8 rows in
     // the chain layout): one 32-element block per thread and turn.
     const int n_rw = (n_expert + 1 + RPW - 1) / RPW;
+    if ((int)blockIdx.x >= n_rw && a.norm_w) {
+        // post_norm first: a half wave per token forms its RMS scale (the
+        // row in registers), then quantises the normalised row, two blocks
+        // per lane, and writes it to hn
+        const int L = threadIdx.x & 31, nhw = NTH / 32;
+        const int nq = gridDim.x - n_rw;
+        for (int t = ((blockIdx.x - n_rw) * gridDim.y + blockIdx.y) * nhw + (threadIdx.x >> 5); t < T;
+             t += nq * gridDim.y * nhw) {
+            const float *g = h + (size_t)t * E;
+            float gv[NS];
+#pragma unroll
+            for (int k = 0; k < NS; k++) gv[k] = g[L + 32 * k];
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NS; k++) acc = fmaf(gv[k], gv[k], acc);
+            const float scale = rms_scale(acc, E, a.eps);
+            for (int b = L; b < E / 32; b += 32) {
+                float v[32];
+                load32(g + 32 * b, v);
+                const float4 *w4 = reinterpret_cast<const float4 *>(a.norm_w + 32 * b);
+                float4 *o4 = reinterpret_cast<float4 *>(a.hn + (size_t)t * E + 32 * b);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float4 w = w4[j];
+                    v[4 * j] = v[4 * j] * (scale * w.x);
+                    v[4 * j + 1] = v[4 * j + 1] * (scale * w.y);
+                    v[4 * j + 2] = v[4 * j + 2] * (scale * w.z);
+                    v[4 * j + 3] = v[4 * j + 3] * (scale * w.w);
+                    o4[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+                }
+                quant_block(v, E, t, b, a.xq, a.xd, a.xs);
+            }
+        }
+        return;
+    }
     if ((int)blockIdx.x >= n_rw) {
         const int nq = gridDim.x - n_rw, nthreads = nq * gridDim.y * blockDim.x;
         for (int i = ((blockIdx.x - n_rw) * gridDim.y + blockIdx.y) * blockDim.x + threadIdx.x; i < T * (E / 32);
@@ -185,6 +235,13 @@ template <int NS, int TC, int NTH = 256> __global__ __launch_bounds__(NTH) void 
     // memory; pieces past the last token reread it into unused LDS)
     __shared__ float xs[TC][E];
     const int t0 = blockIdx.y * TC, nt = min(TC, T - t0);
+    // post_norm: this thread's norm weights, loaded while the tokens stage
+    constexpr int NWPT = E / NTH > 0 ? E / NTH : 1;
+    float nw[NWPT];
+    if (a.norm_w) {
+#pragma unroll
+        for (int j = 0; j < NWPT; j++) nw[j] = (int)threadIdx.x + NTH * j < E ? a.norm_w[threadIdx.x + NTH * j] : 0.0f;
+    }
     {
         constexpr int NP = TC * (E / 4) / NTH; // 16-byte pieces per thread
         const float4 *src = reinterpret_cast<const float4 *>(h + (size_t)t0 * E);
@@ -198,6 +255,29 @@ template <int NS, int TC, int NTH = 256> __global__ __launch_bounds__(NTH) void 
         }
     }
     __syncthreads();
+    if (a.norm_w) {
+        // rms_norm of the staged tokens in place: a half wave per token forms
+        // the scale, then every thread scales its elements, v * (scale * w)
+        __shared__ float scl[TC];
+        const int L = threadIdx.x & 31;
+        for (int t = threadIdx.x >> 5; t < nt; t += NTH / 32) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NS; k++) acc = fmaf(xs[t][L + 32 * k], xs[t][L + 32 * k], acc);
+            const float scale = rms_scale(acc, E, a.eps);
+            if (L == 0) scl[t] = scale;
+        }
+        __syncthreads();
+        for (int t = 0; t < nt; t++) {
+            const float scale = scl[t];
+#pragma unroll
+            for (int j = 0; j < NWPT; j++) {
+                const int e = threadIdx.x + NTH * j;
+                if (e < E) xs[t][e] = xs[t][e] * (scale * nw[j]);
+            }
+        }
+        __syncthreads();
+    }
     auto finish = [&](float acc, int t) {
         float v = acc;
         v = v + __shfl_xor(v, 8);  // acc0+acc1 (lanes 0-7), acc2+acc3 (16-23)
@@ -1901,8 +1981,16 @@ hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, i
 #ifndef BIV_ROUTER_T1_NTH
 #define BIV_ROUTER_T1_NTH 64
 #endif
-hipError_t launch_router(const RouterArgs &a, hipStream_t st)
+hipError_t launch_router(const RouterArgs &a0, hipStream_t st)
 {
+    RouterArgs a = a0;
+    if (a.norm_w && a.T >= RT_MIN_T) {
+        // the tiled router stages tokens a piece at a time: rms_norm into hn first
+        hipError_t e = launch_rms_norm(a.h, a.hn, a.norm_w, a.T, a.E, a.eps, st);
+        if (e != hipSuccess) return e;
+        a.h = a.hn;
+        a.norm_w = nullptr;
+    }
     if (a.T >= RT_MIN_T && a.E % (32 * RT_KC) == 0) {
         const int rows = a.T <= BIV_RT_RB4_T ? 8 : 16;
         const int n_tr = (a.n_expert + 1 + rows - 1) / rows, n_tt = (a.T + RT_TOKS - 1) / RT_TOKS;

@@ -704,32 +704,32 @@ __global__ __launch_bounds__(QNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
                     for (int jr = 0; jr < AJ; jr++) dxs[jr] = dxr[jr];
                     // the A words: low halves under one exec mask, high halves
                     // under the other, exec restored, then a wait for them.
-                    // The control flow here is uniform (every lane active),
-                    // so the masks only narrow exec for the reads.
+                    // The masks are ANDed with the saved exec, so lanes that
+                    // are inactive here stay inactive under either mask.
                     constexpr int PO = 2 * XRS * 8; // bytes from pair to pair
                     static_assert(PO * (NPR - 1) + 128 < 65536, "ds_read offsets are 16-bit");
                     uint64_t ex;
                     if constexpr (AJ == 1) {
-                        asm volatile("s_mov_b64 %0, exec\n\ts_mov_b64 exec, %3\n\t"
+                        asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %3, %0\n\t"
                                      "ds_read_b64 %1, %5 offset:%6\n\t"
-                                     "s_mov_b64 exec, %4\n\t"
+                                     "s_and_b64 exec, %4, %0\n\t"
                                      "ds_read_b64 %2, %5 offset:%6\n\t"
                                      "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
                                      : "=&s"(ex), "+v"(alo[0]), "+v"(ahi[0])
                                      : "s"(mlo), "s"(mhi), "v"(xa), "i"(PO * p)
-                                     : "memory");
+                                     : "memory", "scc");
                     } else {
                         static_assert(AJ == 2, "AJ");
-                        asm volatile("s_mov_b64 %0, exec\n\ts_mov_b64 exec, %5\n\t"
+                        asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %5, %0\n\t"
                                      "ds_read_b64 %1, %7 offset:%8\n\t"
                                      "ds_read_b64 %2, %7 offset:%9\n\t"
-                                     "s_mov_b64 exec, %6\n\t"
+                                     "s_and_b64 exec, %6, %0\n\t"
                                      "ds_read_b64 %3, %7 offset:%8\n\t"
                                      "ds_read_b64 %4, %7 offset:%9\n\t"
                                      "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
                                      : "=&s"(ex), "+v"(alo[0]), "+v"(alo[1]), "+v"(ahi[0]), "+v"(ahi[1])
                                      : "s"(mlo), "s"(mhi), "v"(xa), "i"(PO * p), "i"(PO * p + 128)
-                                     : "memory");
+                                     : "memory", "scc");
                     }
 #pragma unroll
                     for (int jr = 0; jr < AJ; jr++) {

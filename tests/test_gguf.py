@@ -173,3 +173,59 @@ def test_dense_config(tmp_path):
         with pytest.raises(HipError) as e:
             g.dense_config()
         assert e.value.code == gguf.E_TYPE
+
+
+def _s(x):
+    b = x.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def _hand_file(tensor_infos, alignment=64):
+    """A GGUF v3 file assembled byte by byte here (not by biv_amd.gguf.write):
+    header, three key/values (the alignment as u32, an array of strings, an
+    f32), the tensor infos, zero padding to the alignment, then the data."""
+    kv = [
+        _s("general.alignment") + struct.pack("<I", 4) + struct.pack("<I", alignment),
+        _s("t.strs") + struct.pack("<I", 9) + struct.pack("<IQ", 8, 3) + _s("ab") + _s("") + _s("cde"),
+        _s("t.f") + struct.pack("<I", 6) + struct.pack("<f", -1.5),
+    ]
+    head = b"GGUF" + struct.pack("<IQQ", 3, len(tensor_infos), len(kv)) + b"".join(kv)
+    for name, dims, ty, off in tensor_infos:
+        head += _s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        head += struct.pack("<IQ", ty, off)
+    start = (len(head) + alignment - 1) // alignment * alignment
+    return head + b"\0" * (start - len(head)), start
+
+
+def test_hand_assembled_fixture(tmp_path):
+    """Tensor-info offsets relative to the aligned data start, an array of
+    strings skipped over, and the padding, on bytes written by hand."""
+    f32 = np.arange(8, dtype=np.float32) * 0.5           # [4, 2] F32 at offset 0
+    q8 = bytes([0x00, 0x3C]) + bytes(range(256 - 16, 256)) + bytes(range(16))  # one Q8_0 block, d = 1.0
+    head, start = _hand_file([("w0", [4, 2], 0, 0), ("w1", [32, 1], 8, 64)])
+    body = f32.tobytes() + b"\0" * 32 + q8 + b"\0" * 30
+    p = tmp_path / "hand.gguf"
+    p.write_bytes(head + body)
+    assert start % 64 == 0 and len(head) == start
+    with gguf.Gguf(str(p)) as g:
+        assert g.tensor_names() == ["w0", "w1"]
+        assert g.get_f32("t.f") == -1.5 and g.get_u64("general.alignment") == 64
+        ty, dims, data = g.tensor("w0")
+        assert ty == 0 and list(dims) == [4, 2]
+        assert np.array_equal(np.frombuffer(bytes(data), np.float32), f32)
+        ty, dims, data = g.tensor("w1")
+        assert ty == 8 and list(dims) == [32, 1] and bytes(data) == q8
+
+
+@pytest.mark.parametrize("dims, ty, why", [([33, 1], 8, "whole blocks"), ([2 ** 40, 2 ** 40], 0, "too large"),
+                                           ([4, 2], 0, "out of bounds")])
+def test_hand_assembled_bad_tensor(tmp_path, dims, ty, why):
+    """A Q8_0 tensor of 33 elements (not whole blocks), dims whose product
+    overflows, and data past the end of the file: each is Error::Truncated-
+    like (E_FORMAT), none reaches an upload."""
+    head, _ = _hand_file([("w", dims, ty, 0)])
+    p = tmp_path / "bad.gguf"
+    p.write_bytes(head + (b"\0" * 16 if why == "out of bounds" else b"\0" * 64))
+    with pytest.raises(HipError) as e:
+        gguf.Gguf(str(p))
+    assert e.value.code == gguf.E_FORMAT and why in str(e.value), str(e.value)

@@ -116,7 +116,7 @@ def full_parity(orc, engine, layer, moe, h, block_dots=True, min_exact=0.9999):
     return rel, t
 
 
-@pytest.mark.parametrize("T", [1, 2, 5, 9, 64, 65, 100])
+@pytest.mark.parametrize("T", [1, 2, 5, 9, 64, 65, 100, 1100])
 def test_q8_small_layer(orc, engine, T):
     """T <= 16 quantises the SwiGLU intermediate inside the down kernel,
     larger T in its own launch; below 64 every sum runs in the x86 order and
@@ -127,6 +127,8 @@ def test_q8_small_layer(orc, engine, T):
     print(f"case q8 small T={T}", flush=True)
     layer, moe = layer_for(engine, seed=21, n_expert=32)
     h = synth.make_tokens(100 + T, T, offsets=True)
+    # T = 1100: 69 blocks of 16 tokens, so a dispatch-scan thread sums a run
+    # of 18 blocks ending in a partial group of 16
     full_parity(orc, engine, layer, moe, h, block_dots=T <= 9 or T in (64, 65),
                 min_exact=0.9999 if T < 64 else 0.0)
 
@@ -227,6 +229,41 @@ def test_rms_norm(orc, engine, n):
         got = engine.rms_norm(x, w, eps)
         ref = orc.rms_norm(x, w, eps)
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), eps
+
+
+@pytest.mark.parametrize("T", [1, 5, 300, 512])
+def test_q8_ffn_step(orc, engine, T):
+    """The FFN half of Model::layer on a Q8_0 layer (model.rs:786-790):
+    x += moe(rms_norm(x, post_norm)).  Below 256 tokens the router launch
+    forms the norm itself (its workgroups normalise the staged rows, the
+    quantising ones write the normalised rows); from 256 a norm launch runs
+    first.  Full-size layer (256 experts); T = 512 with Zipf-skewed routing."""
+    print(f"case q8 ffn_step T={T}", flush=True)
+    layer, moe = layer_for(engine, seed=1)
+    E, eps = layer.n_embd, 1e-6
+    rng = np.random.default_rng(900 + T)
+    w = (1.0 + 0.05 * rng.standard_normal(E)).astype(np.float32)
+    x = synth.zipf_bias_tokens(layer, 910, T) if T >= 512 else synth.make_tokens(910 + T, T, offsets=T > 1)
+    x = (x * np.float32(3.0)).astype(np.float32)  # rows of RMS ~3: the norm matters
+    xd, nd = engine.malloc(x.nbytes), engine.malloc(E * 4)
+    try:
+        engine.h2d(xd, x)
+        engine.h2d(nd, w)
+        moe.ffn_step_device(xd, nd, eps, T)
+        got = engine.d2h(np.empty_like(x), xd)
+        hn = orc.rms_norm(x, w, eps)
+        routed = orc.moe(layer, hn, threads=8)
+        ref = x + routed
+        # the block's share alone, against the oracle's block output
+        check_output(routed, got - x, min_exact=0.0)
+        check_output(ref, got, min_exact=0.9999 if T < 64 else 0.0)
+        engine.h2d(xd, x)
+        moe.ffn_step_device(xd, nd, eps, T)
+        again = engine.d2h(np.empty_like(x), xd)
+        assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "not bit-identical run to run"
+    finally:
+        engine.free(xd)
+        engine.free(nd)
 
 
 def test_bf16_stack_steps(orc, engine):
