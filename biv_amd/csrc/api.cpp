@@ -13,6 +13,7 @@
 #include <cstring>
 #include <string>
 #include <thread>
+#include <type_traits>
 #include <vector>
 
 using biv::DevMat;
@@ -91,6 +92,8 @@ struct biv_hip_ctx {
     bool fused_dc = true;
     std::vector<hipEvent_t> ev_pool;
     std::vector<std::vector<hipEvent_t>> ev_fwd;
+    // this GPU's copy of the no-allocation scratch (hipGetSymbolAddress)
+    uint8_t *noalloc = nullptr;
 };
 
 namespace {
@@ -386,6 +389,39 @@ void scratch_free(biv_hip_ctx *ctx)
     ctx->sc = Scratch{};
 }
 
+// The buffers of one forward of up to cap tokens of a layer of the given
+// shape: take(ptr, count) is called for each, in one fixed order.
+template <class Take>
+int scratch_plan(Scratch &s, size_t cap, size_t E, size_t ff, size_t ne, size_t k, Take take)
+{
+    const size_t P = cap * k, R = P + cap;
+    int rc = 0;
+    rc = rc ? rc : take(s.xq, cap * E);
+    rc = rc ? rc : take(s.xd, cap * E / 32);
+    rc = rc ? rc : take(s.xs, cap * E / 32);
+    rc = rc ? rc : take(s.logits, cap * ne);
+    rc = rc ? rc : take(s.glogit, cap);
+    rc = rc ? rc : take(s.act, R * ff);
+    rc = rc ? rc : take(s.aq, R * ff);
+    rc = rc ? rc : take(s.ad, R * ff / 32);
+    rc = rc ? rc : take(s.as, R * ff / 32);
+    rc = rc ? rc : take(s.y, R * E);
+    rc = rc ? rc : take(s.h_stage, cap * E);
+    // bf16 halves of h or of the intermediate, whichever is larger
+    rc = rc ? rc : take(s.xh, 2 * std::max(cap * E, R * ff));
+    rc = rc ? rc : take(s.xl, 2 * std::max(cap * E, R * ff));
+    rc = rc ? rc : take(s.o_stage, cap * E);
+    rc = rc ? rc : take(s.dp.slots, ne + P); // >= max_slots(ne, P, chunk)
+    rc = rc ? rc : take(s.dp.pair_tok, P);
+    rc = rc ? rc : take(s.dp.pair_exp, P);
+    rc = rc ? rc : take(s.dp.pair_w, P);
+    rc = rc ? rc : take(s.dp.tok_pairs, P);
+    rc = rc ? rc : take(s.dp.ids, P);
+    rc = rc ? rc : take(s.dp.wts, P);
+    rc = rc ? rc : take(s.counters, biv::route_work_ints((int)cap));
+    return rc;
+}
+
 // Make the scratch fit T tokens of layer m.
 int scratch_fit(biv_hip_ctx *ctx, const biv_hip_moe *m, int T)
 {
@@ -400,37 +436,48 @@ int scratch_fit(biv_hip_ctx *ctx, const biv_hip_moe *m, int T)
     ctx->sc_ff = std::max(ctx->sc_ff, m->ff);
     ctx->sc_ne = std::max(ctx->sc_ne, m->n_expert);
     ctx->sc_k = std::max(ctx->sc_k, m->k);
-    const size_t E = ctx->sc_E, ff = ctx->sc_ff, ne = ctx->sc_ne, k = ctx->sc_k;
-    const size_t P = (size_t)cap * k, R = P + cap;
-    int rc = 0;
-    rc = rc ? rc : sc_alloc(ctx, cap * E, &s.xq);
-    rc = rc ? rc : sc_alloc(ctx, cap * E / 32, &s.xd);
-    rc = rc ? rc : sc_alloc(ctx, cap * E / 32, &s.xs);
-    rc = rc ? rc : sc_alloc(ctx, cap * ne, &s.logits);
-    rc = rc ? rc : sc_alloc(ctx, (size_t)cap, &s.glogit);
-    rc = rc ? rc : sc_alloc(ctx, R * ff, &s.act);
-    rc = rc ? rc : sc_alloc(ctx, R * ff, &s.aq);
-    rc = rc ? rc : sc_alloc(ctx, R * ff / 32, &s.ad);
-    rc = rc ? rc : sc_alloc(ctx, R * ff / 32, &s.as);
-    rc = rc ? rc : sc_alloc(ctx, R * E, &s.y);
-    rc = rc ? rc : sc_alloc(ctx, cap * E, &s.h_stage);
-    // bf16 halves of h or of the intermediate, whichever is larger
-    rc = rc ? rc : sc_alloc(ctx, 2 * std::max((size_t)cap * E, R * ff), &s.xh);
-    rc = rc ? rc : sc_alloc(ctx, 2 * std::max((size_t)cap * E, R * ff), &s.xl);
-    rc = rc ? rc : sc_alloc(ctx, cap * E, &s.o_stage);
-    rc = rc ? rc : sc_alloc(ctx, ne + P, &s.dp.slots); // >= max_slots(ne, P, chunk)
-    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_tok);
-    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_exp);
-    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.pair_w);
-    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.tok_pairs);
-    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.ids);
-    rc = rc ? rc : sc_alloc(ctx, P, &s.dp.wts);
-    rc = rc ? rc : sc_alloc(ctx, biv::route_work_ints(cap), &s.counters);
+    int rc = scratch_plan(s, cap, ctx->sc_E, ctx->sc_ff, ctx->sc_ne, ctx->sc_k,
+                          [&](auto *&p, size_t count) { return sc_alloc(ctx, count, &p); });
     if (rc) {
         scratch_free(ctx);
         return rc;
     }
     s.cap_T = cap;
+    return 0;
+}
+
+// The scratch of biv_hip_moe_forward_device_noalloc: device memory the
+// library holds from load to process end, one copy per GPU, so that this
+// entry point calls no allocator.  Host code never passes `scratch` itself
+// (on the host it names a stand-in, not a device address): each context
+// resolves its GPU's copy with hipGetSymbolAddress at creation and uses that.
+constexpr size_t NOALLOC_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
+
+// Carve the buffers of a forward of T tokens of layer m out of the context's
+// copy of `scratch` (256-byte aligned pieces).  No allocation.
+int noalloc_scratch(biv_hip_ctx *ctx, const biv_hip_moe *m, int T, Scratch &s);
+
+int noalloc_scratch(biv_hip_ctx *ctx, const biv_hip_moe *m, int T, Scratch &s)
+{
+    size_t off = 0;
+    bool fits = true;
+    auto take = [&](auto *&p, size_t count) {
+        using Elem = std::remove_reference_t<decltype(*p)>;
+        off = (off + 255) & ~(size_t)255;
+        const size_t bytes = count * sizeof(Elem) + 16;
+        if (off + bytes > NOALLOC_BYTES) fits = false;
+        p = fits ? reinterpret_cast<Elem *>(ctx->noalloc + off) : nullptr;
+        off += bytes;
+        return 0;
+    };
+    s = Scratch{};
+    scratch_plan(s, (size_t)T, m->E, m->ff, m->n_expert, m->k, take);
+    if (!fits)
+        return fail(ctx, BIV_HIP_E_INVALID,
+                    "%d tokens of this layer need %zu bytes of scratch; the no-allocation entry point has %zu", T, off,
+                    NOALLOC_BYTES);
+    s.cap_T = T;
     return 0;
 }
 
@@ -478,16 +525,17 @@ struct StageMarks {
 // With norm_w, h is the residual x and the block takes rms_norm(x) with
 // these weights (the post_norm of model.rs:786-790), formed by the router
 // launch into the scratch row block h_stage.
+// ext: run in these scratch buffers (sized for T) instead of the context's.
 int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float *out, unsigned flags,
-            const Dumps &dm, int only = -1, const float *norm_w = nullptr, float eps = 0.0f)
+            const Dumps &dm, int only = -1, const float *norm_w = nullptr, float eps = 0.0f, Scratch *ext = nullptr)
 {
     if (T == 0) return 0;
-    int rc = scratch_fit(ctx, m, T);
+    int rc = ext ? 0 : scratch_fit(ctx, m, T);
     if (rc) return rc;
     StageMarks mk(ctx);
 #define MARK() HIP_TRY(ctx, only < 0 ? mk.mark() : hipSuccess, "timing event")
     auto run = [&](int stage) { return only < 0 || only == stage; };
-    Scratch &s = ctx->sc;
+    Scratch &s = ext ? *ext : ctx->sc;
     hipStream_t st = ctx->stream;
     const int E = m->E, ff = m->ff, ne = m->n_expert, k = m->k;
     const int P = T * k;
@@ -699,6 +747,13 @@ int biv_hip_create(int device, biv_hip_ctx **out)
         return fail(nullptr, BIV_HIP_E_DEVICE, "stream: %s", hipGetErrorString(e));
     }
     ctx->stream = ctx->own;
+    // the device address of this GPU's no-allocation scratch (device is current)
+    e = hipGetSymbolAddress(reinterpret_cast<void **>(&ctx->noalloc), HIP_SYMBOL(scratch));
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(ctx->own);
+        delete ctx;
+        return fail(nullptr, BIV_HIP_E_DEVICE, "no-allocation scratch address: %s", hipGetErrorString(e));
+    }
     const char *fdc = getenv("BIV_HIP_FUSED_DC");
     ctx->fused_dc = !(fdc && fdc[0] == '0');
     *out = ctx;
@@ -848,6 +903,18 @@ int biv_hip_moe_forward_device(biv_hip_ctx *ctx, const biv_hip_moe *moe, const f
     if (rc) return rc;
     HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
     return forward(ctx, moe, h_dev, n, out_dev, flags, Dumps{});
+}
+
+int biv_hip_moe_forward_device_noalloc(biv_hip_ctx *ctx, const biv_hip_moe *moe, const float *h_dev, int n,
+                                       float *out_dev, unsigned flags)
+{
+    int rc = check_fwd(ctx, moe, h_dev, n, out_dev);
+    if (rc) return rc;
+    if (n == 0) return 0;
+    HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    Scratch s;
+    if ((rc = noalloc_scratch(ctx, moe, n, s))) return rc;
+    return forward(ctx, moe, h_dev, n, out_dev, flags, Dumps{}, -1, nullptr, 0.0f, &s);
 }
 
 int biv_hip_moe_forward_taps(biv_hip_ctx *ctx, const biv_hip_moe *moe, const float *h, int n, float *out,

@@ -29,7 +29,7 @@ ADD = 1
 SYMBOLS = [
     "biv_hip_create", "biv_hip_destroy", "biv_hip_last_error", "biv_hip_set_stream", "biv_hip_sync",
     "biv_hip_upload_weight", "biv_hip_upload_experts", "biv_hip_moe_create", "biv_hip_moe_forward",
-    "biv_hip_moe_forward_device", "biv_hip_moe_forward_taps", "biv_hip_malloc", "biv_hip_free",
+    "biv_hip_moe_forward_device", "biv_hip_moe_forward_device_noalloc", "biv_hip_moe_forward_taps", "biv_hip_malloc", "biv_hip_free",
     "biv_hip_memcpy_h2d", "biv_hip_memcpy_d2h", "biv_hip_numerics", "biv_hip_device_bytes",
     "biv_hip_set_timing", "biv_hip_stage_times", "biv_hip_time_stage", "biv_hip_rms_norm",
     "biv_hip_moe_ffn_step", "biv_hip_moe_from_gguf", "biv_hip_dense_create", "biv_hip_dense_forward",
@@ -78,6 +78,7 @@ def load():
     L.biv_hip_moe_create.argtypes = [vp] + [vp] * 8 + [i, pp]
     L.biv_hip_moe_forward.argtypes = [vp, vp, vp, i, vp, ctypes.c_uint]
     L.biv_hip_moe_forward_device.argtypes = [vp, vp, vp, i, vp, ctypes.c_uint]
+    L.biv_hip_moe_forward_device_noalloc.argtypes = [vp, vp, vp, i, vp, ctypes.c_uint]
     L.biv_hip_moe_forward_taps.argtypes = [vp, vp, vp, i, vp, ctypes.c_uint, ctypes.POINTER(Taps)]
     L.biv_hip_malloc.argtypes = [vp, sz, pp]
     L.biv_hip_free.argtypes = [vp, vp]
@@ -159,6 +160,14 @@ class HipMoe:
         """encode_moe's counterpart: device pointers, queued on the context's stream."""
         self.ctx._check(self.ctx.L.biv_hip_moe_forward_device(self.ctx.h, self.handle, ctypes.c_void_p(h_dev), n,
                                                               ctypes.c_void_p(out_dev), ADD if add else 0))
+
+
+    def forward_device_noalloc(self, h_dev, n, out_dev, add=False):
+        """forward_device through the entry point that allocates nothing (its
+        scratch is the library's fixed device buffer, shared by every call on
+        the GPU)."""
+        self.ctx._check(self.ctx.L.biv_hip_moe_forward_device_noalloc(
+            self.ctx.h, self.handle, ctypes.c_void_p(h_dev), n, ctypes.c_void_p(out_dev), ADD if add else 0))
 
 
 class HipDense:
