@@ -478,31 +478,40 @@ __global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
 // fma(float(word dot), w_scale(b) * d_x(b), acc); then the chains are summed
 // in a fixed tree, and Q4_K subtracts its mins term last (the chain kernels
 // in kernels.hip do exactly this on the vector ALU).  Here
-// v_mfma_f32_16x16x32_f16 produces the word dots, already as f32: its A
-// operand is the block of two input rows, masked so that A row 8 tt + l
-// keeps only word l of input row tt; its B operand is the block of 16 weight
-// rows (8 gate rows, then the same 8 rows of up).  Both hold the quants
-// (Q4_K: nibbles 0..15) as f16, which is exact for integers this small;
-// every product is exact and every partial sum an integer below 2^17, so D
-// row 8 tt + l, column n is the word-l dot of input row tt and weight row n,
-// exactly, and equal to the reference's float(int32 word dot) without a
-// convert.  The vector ALU does what remains, in the reference's order: fma
-// into the chain, tree, mins, SwiGLU.
+// v_mfma_f32_32x32x16_f16 produces the word dots, already as f32, 1024 per
+// instruction: K = 16 is half a block (words 4 hh .. 4 hh + 3); the A
+// operand holds 8 input rows, each four times, A row 4 t + w keeping only
+// word 4 hh + w of input row t (the other 12 of its 16 values are zero); the
+// B operand holds 32 weight rows (16 rows of gate, then the same 16 of up).
+// Both hold the quants (Q4_K: nibbles 0..15) as f16, exact for integers
+// this small; every product is exact and every partial sum an integer below
+// 2^17, so D row 4 t + w, column n is the word dot of input row t and weight
+// row n, exactly, and equal to the reference's float(int32 word dot).  The
+// vector ALU does what remains, in the reference's order: fma into the
+// chain, the tree, the mins, the SwiGLU.
 //
-// D of an MFMA: lane (n, kq) holds column n and A rows 4 kq .. 4 kq + 3,
-// i.e. input row kq / 2 of the pair, words 4 (kq & 1) .. + 3: eight chains
-// (two parities x four words) of one (input row, weight row); the other
-// eight are in lane (n, kq ^ 1).
+// D of the MFMA: lane (n, kg) (n = lane % 32, kg = lane / 32) holds column n
+// and rows 8 q + 4 kg + r (q, r = 0..3), i.e. words 4 hh + r of input rows
+// 2 q + kg: so a lane ends up holding all 16 chains of 4 input rows of its
+// 8-row tile with weight row n, and the tree runs within the lane.
 //
-// A workgroup takes a slot (up to QT pairs, MFMA_Q8_TILE, staged in LDS)
-// and QW waves of 8 output rows; a wave streams its 16 weight rows a step
-// ahead and keeps the chains of all pairs of the slot in registers.
+// A workgroup takes a slot (up to QT = 16 pairs, staged in LDS as f16 words:
+// two 8-row tiles) and 4 waves of 16 output rows; a wave streams its 32
+// weight rows one step ahead and keeps the chains of the slot's pairs in
+// registers (2 tiles x 4 rows x 16 chains).  The weight operands are
+// converted to f16 once per half block and meet both tiles.
+constexpr int GW = 4;               // waves of a workgroup
+constexpr int GNTH = GW * 64;
+constexpr int G_ROWS_WG = GW * 16;  // output rows of a workgroup
+constexpr int GNT = QT / 8;         // 8-row tiles of a slot
 
 // Weight operands of the exact kernel.  A step covers the blocks 8 g + pi +
 // 2 j (j = 0..3) of one parity (Q8_0: a half-group) or both parities (Q4_K:
-// super-block g, whose nibble bytes serve both).  operand(w, pi, j) is the
-// lane's 8 quants of block 8 g + pi + 2 j as exact f16; scale(w, pi, j)
-// its f32 weight scale as the reference forms it.
+// super-block g, whose nibble bytes serve both).  Lane kg of a column takes
+// words 2 kg, 2 kg + 1 (half 0) and 4 + 2 kg, 5 + 2 kg (half 1) of each
+// block.  operand(w, pi, j, hh) is its 8 quants of half hh of block
+// 8 g + pi + 2 j as exact f16; scale(w, pi, j) the block's f32 weight scale
+// as the reference forms it.
 template <int TY, int K> struct GuW;
 
 // Q8_0 (chain layout: unit 16 g + 8 pi + w holds word w of the blocks
@@ -511,25 +520,28 @@ template <int K> struct GuW<T_Q8_0, K> {
     static constexpr int STEPS = K / 128; // half-groups
     static constexpr bool BOTH = false;  // a step is one parity
     struct Step {
-        uint4 q[2];
+        uint4 q[4]; // units 2 kg, 2 kg + 1, 4 + 2 kg, 5 + 2 kg of the half-group
         uint2 s;
     };
     const uint4 *wq;
     const uint2 *wsc;
-    __device__ GuW(const uint8_t *q, const uint8_t *s, size_t row, int kq)
-        : wq(reinterpret_cast<const uint4 *>(q + row * K) + 2 * kq),
+    __device__ GuW(const uint8_t *q, const uint8_t *s, size_t row, int kg)
+        : wq(reinterpret_cast<const uint4 *>(q + row * K) + 2 * kg),
           wsc(reinterpret_cast<const uint2 *>(s + row * (K / 32) * 2)) {}
     __device__ void load(int h, Step &w) const
     {
         const int g = h >> 1, pi = h & 1;
-        w.q[0] = wq[16 * g + 8 * pi];
-        w.q[1] = wq[16 * g + 8 * pi + 1];
+        const uint4 *p = wq + 16 * g + 8 * pi;
+        w.q[0] = p[0];
+        w.q[1] = p[1];
+        w.q[2] = p[4];
+        w.q[3] = p[5];
         w.s = wsc[(pi * (K / 64) + 4 * g) / 4];
     }
-    __device__ static uint4 operand(const Step &w, int pi, int j)
+    __device__ static f16x8 operand(const Step &w, int pi, int j, int hh)
     {
-        const uint2 lo = i8x4_to_f16x4(w.q[0][j]), hi = i8x4_to_f16x4(w.q[1][j]);
-        return make_uint4(lo.x, lo.y, hi.x, hi.y);
+        const uint2 lo = i8x4_to_f16x4(w.q[2 * hh][j]), hi = i8x4_to_f16x4(w.q[2 * hh + 1][j]);
+        return __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
     }
     __device__ static float scale(const Step &w, int pi, int j)
     {
@@ -545,25 +557,28 @@ template <int K> struct GuW<T_Q4K, K> {
     static constexpr int STEPS = K / 256; // super-blocks
     static constexpr bool BOTH = true;
     struct Step {
-        uint4 q[2];
+        uint4 q[4];
         int4 hd; // d, dmin, the 12 scale bytes
     };
     const uint4 *wq;
     const int4 *whd;
-    __device__ GuW(const uint8_t *q, const uint8_t *s, size_t row, int kq)
-        : wq(reinterpret_cast<const uint4 *>(q + row * (K / 2)) + 2 * kq),
+    __device__ GuW(const uint8_t *q, const uint8_t *s, size_t row, int kg)
+        : wq(reinterpret_cast<const uint4 *>(q + row * (K / 2)) + 2 * kg),
           whd(reinterpret_cast<const int4 *>(s + row * (K / 256) * 16)) {}
     __device__ void load(int g, Step &w) const
     {
-        w.q[0] = wq[8 * g];
-        w.q[1] = wq[8 * g + 1];
+        const uint4 *p = wq + 8 * g;
+        w.q[0] = p[0];
+        w.q[1] = p[1];
+        w.q[2] = p[4];
+        w.q[3] = p[5];
         w.hd = whd[g];
     }
-    __device__ static uint4 operand(const Step &w, int pi, int j)
+    __device__ static f16x8 operand(const Step &w, int pi, int j, int hh)
     {
-        const uint2 lo = bytes_to_f16x4<1024>((w.q[0][j] >> (4 * pi)) & 0x0F0F0F0Fu);
-        const uint2 hi = bytes_to_f16x4<1024>((w.q[1][j] >> (4 * pi)) & 0x0F0F0F0Fu);
-        return make_uint4(lo.x, lo.y, hi.x, hi.y);
+        const uint2 lo = bytes_to_f16x4<1024>((w.q[2 * hh][j] >> (4 * pi)) & 0x0F0F0F0Fu);
+        const uint2 hi = bytes_to_f16x4<1024>((w.q[2 * hh + 1][j] >> (4 * pi)) & 0x0F0F0F0Fu);
+        return __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
     }
     __device__ static float scale(const Step &w, int pi, int j)
     {
@@ -575,35 +590,27 @@ template <int K> struct GuW<T_Q4K, K> {
     }
 };
 
+// two workgroups per CU (LDS: 70 KB each at K = 2048), two waves per SIMD
 template <int TY, int K, bool DUMP>
-#ifndef GU_EXACT_AJ
-#define GU_EXACT_AJ 2 // blocks per LDS read group, Q8_0
-#endif
-#ifndef GU_EXACT_AJ_Q4K
-#define GU_EXACT_AJ_Q4K 2 // and Q4_K
-#endif
-// four waves per SIMD (two workgroups per CU, as the LDS allows): the
-// registers are held to 128 (Q4_K then spills 6 of them to scratch, still
-// faster than three waves per SIMD without spills)
-__global__ __launch_bounds__(QNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 : 4))) void k_gu_exact(MvArgs a)
+__global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 : 2))) void k_gu_exact(MvArgs a)
 {
     using W = GuW<TY, K>;
     constexpr int NB = K / 32;
-    constexpr int NPR = QT / 2;      // input-row pairs of a slot
-    constexpr int DSTR = NB + 4;     // staged scales [row][q8_scale order]: floats (16-byte aligned rows)
     constexpr bool Q4K = TY == T_Q4K;
-    static_assert(QT % 2 == 0, "pairs of input rows");
-    constexpr int AJ = Q4K ? GU_EXACT_AJ_Q4K : GU_EXACT_AJ;          // blocks per A read group
     // The input rows' words as exact f16: word l of block b of input row i
-    // (four values, 8 bytes) at xop_s[i * XRS + 8 b + l].  Rows are XRS
-    // entries apart, 64 bytes more than their words, so that the two rows of
-    // a pair sit in different LDS banks.
-    constexpr int XRS = NB * 8 + 8;
+    // (four values, 8 bytes) at xop_s[i * XRS + 8 b + l].  Rows are 32 bytes
+    // more than their words apart: the 16 lanes of a masked read (rows 0..7,
+    // two words) then fall in distinct banks.
+    constexpr int XRS = NB * 8 + 4;
+    // Block scales of the input rows, [q8_scale order][tile][kg][q] for row
+    // 8 tile + 2 q + kg: a lane's four rows in one 16-byte read.
+    constexpr int DSTR = QT + 4;
+    constexpr int SSTR = NB + 4; // Q4_K block sums [row][q8_scale order]
     __shared__ uint2 xop_s[QT * XRS];
-    __shared__ float xd_s[QT * DSTR];
-    __shared__ float xs_s[Q4K ? QT * DSTR : 1]; // Q4_K: d * sum(q) of each block, for the mins
+    __shared__ float xd_s[NB * DSTR];
+    __shared__ float xs_s[Q4K ? QT * SSTR : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n = lane & 15, kq = lane >> 4;
+    const int li = lane & 31, kg = lane >> 5;
     const int G = N_XCD * a.n_rt, bid = blockIdx.x;
     const int u = (bid / G) * N_XCD + bid % N_XCD, rt = (bid % G) / N_XCD;
     if (u >= a.u_max + a.n_sh) return;
@@ -623,166 +630,49 @@ __global__ __launch_bounds__(QNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
     const DevMat &M = shared ? a.sa : a.a;
     const DevMat &B = shared ? a.sb : a.b;
     const int rows = M.rows;
-    // this lane's weight row: column n of the MFMA tile, gate rows then up
-    const int orow = rt * (QW * 8) + wave * 8 + (n & 7);
+    // this lane's weight row: column li of the MFMA tile, gate rows then up
+    const int orow = rt * G_ROWS_WG + wave * 16 + (li & 15);
     const size_t wr = (size_t)e * rows + orow;
-    const W wsrc(n < 8 ? M.q : B.q, n < 8 ? M.s : B.s, wr, kq);
-    typename W::Step w0, w1;
+    const W wsrc(li < 16 ? M.q : B.q, li < 16 ? M.s : B.s, wr, kg);
+    typename W::Step w0;
     wsrc.load(0, w0); // the first weights go out before the staging waits
-    // stage the slot's input rows: the masked A operands (from the chain
-    // layout: unit 16 g + 8 pi + l holds word l of blocks 8 g + pi + 2 j) and
-    // block scales (and Q4_K's block sums) [row][q8_scale order]; rows past
-    // the count repeat the last one (their results are not stored)
+    // stage the slot's input rows: f16 words (from the chain layout: unit
+    // 16 g + 8 pi + l holds word l of blocks 8 g + pi + 2 j), block scales
+    // (and Q4_K's block sums); rows past the count repeat the last one (their
+    // results are not stored)
     {
         constexpr int UPR = K / 16; // units per row
-        for (int idx = tid; idx < QT * UPR; idx += QNTH) {
+        for (int idx = tid; idx < QT * UPR; idx += GNTH) {
             const int i = idx / UPR, c = idx % UPR;
             const int ti = min(i, cnt - 1);
             const size_t ar = shared ? (size_t)(tok0 + ti) : (size_t)a.dp.pair_tok[beg + ti];
             const uint4 v = reinterpret_cast<const uint4 *>(a.xq + ar * K)[c];
             const int g = c >> 4, pi = (c >> 3) & 1, l = c & 7;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int b = 8 * g + pi + 2 * j;
-                xop_s[i * XRS + b * 8 + l] = i8x4_to_f16x4(v[j]);
-            }
+            for (int j = 0; j < 4; j++) xop_s[i * XRS + (8 * g + pi + 2 * j) * 8 + l] = i8x4_to_f16x4(v[j]);
         }
-        for (int idx = tid; idx < QT * NB; idx += QNTH) {
+        for (int idx = tid; idx < QT * NB; idx += GNTH) {
             const int i = idx / NB, bs = idx % NB;
             const int ti = min(i, cnt - 1);
             const size_t ar = shared ? (size_t)(tok0 + ti) : (size_t)a.dp.pair_tok[beg + ti];
-            xd_s[i * DSTR + bs] = a.xd[ar * NB + bs];
-            if (Q4K) xs_s[i * DSTR + bs] = a.xs[ar * NB + bs];
+            xd_s[bs * DSTR + (i >> 3) * 8 + (i & 1) * 4 + ((i & 7) >> 1)] = a.xd[ar * NB + bs];
+            if (Q4K) xs_s[i * SSTR + bs] = a.xs[ar * NB + bs];
         }
     }
     __syncthreads();
-    // the A operand: A row 8 tt + l keeps word l of input row tt, which lane
-    // kq = l / 2 holds in its low half (l even) or high half (l odd); every
-    // other half of every lane is zero.  The registers start at zero and the
-    // lanes load only their own half (reads under an exec mask), so the
-    // zeros stay and no lane reads LDS for them.
-    const int tt = (n >> 3), l = n & 7;
-    const bool mine = (l >> 1) == kq;
-    const uint64_t mlo = __ballot(mine && !(l & 1)), mhi = __ballot(mine && (l & 1));
-    const uint32_t xa0 = (uint32_t)reinterpret_cast<uintptr_t>(xop_s + tt * XRS + l);
-    uint64_t alo[AJ], ahi[AJ];
-#pragma unroll
-    for (int j = 0; j < AJ; j++) alo[j] = ahi[j] = 0ull;
-    // this lane's D: input row kq / 2 of the pair, chains (pi, 4 (kq & 1) + jj)
-    const int drow = kq >> 1;
-    float acc[NPR][2][4];
-#pragma unroll
-    for (int p = 0; p < NPR; p++)
-#pragma unroll
-        for (int pi = 0; pi < 2; pi++)
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) acc[p][pi][jj] = 0.0f;
-    // the blocks 8 g + pi + 2 j, j = 0..3, of parity pi (a compile-time
-    // constant: it picks the chain accumulators)
-    auto compute = [&](int g, auto pi_c, const typename W::Step &w) {
-        constexpr int pi = decltype(pi_c)::value;
-        // AJ blocks at a time: their weight operands converted once, then
-        // met with every pair of the slot
-#pragma unroll
-        for (int j0 = 0; j0 < 4; j0 += AJ) {
-            float dw[AJ];
-            f16x8 wo[AJ];
-#pragma unroll
-            for (int jr = 0; jr < AJ; jr++) {
-                dw[jr] = W::scale(w, pi, j0 + jr);
-                wo[jr] = __builtin_bit_cast(f16x8, W::operand(w, pi, j0 + jr));
-            }
-            // this lane's words of pair 0, blocks 8 g + pi + 2 j0 ..
-            const uint32_t xa = xa0 + ((8 * g + pi) * 8 + 16 * j0) * 8;
-#pragma unroll
-            for (int p = 0; p < NPR; p++) {
-                if (2 * p < cnt) { // uniform
-                    // d_x of the blocks for this lane's D row (input row 2 p + drow)
-                    const float *dxr = xd_s + (2 * p + drow) * DSTR + pi * (K / 64) + 4 * g + j0;
-                    float dxs[AJ];
-#pragma unroll
-                    for (int jr = 0; jr < AJ; jr++) dxs[jr] = dxr[jr];
-                    // the A words: low halves under one exec mask, high halves
-                    // under the other, exec restored, then a wait for them.
-                    // The masks are ANDed with the saved exec, so lanes that
-                    // are inactive here stay inactive under either mask.
-                    constexpr int PO = 2 * XRS * 8; // bytes from pair to pair
-                    static_assert(PO * (NPR - 1) + 128 < 65536, "ds_read offsets are 16-bit");
-                    uint64_t ex;
-                    if constexpr (AJ == 1) {
-                        asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %3, %0\n\t"
-                                     "ds_read_b64 %1, %5 offset:%6\n\t"
-                                     "s_and_b64 exec, %4, %0\n\t"
-                                     "ds_read_b64 %2, %5 offset:%6\n\t"
-                                     "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
-                                     : "=&s"(ex), "+v"(alo[0]), "+v"(ahi[0])
-                                     : "s"(mlo), "s"(mhi), "v"(xa), "i"(PO * p)
-                                     : "memory", "scc");
-                    } else {
-                        static_assert(AJ == 2, "AJ");
-                        asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %5, %0\n\t"
-                                     "ds_read_b64 %1, %7 offset:%8\n\t"
-                                     "ds_read_b64 %2, %7 offset:%9\n\t"
-                                     "s_and_b64 exec, %6, %0\n\t"
-                                     "ds_read_b64 %3, %7 offset:%8\n\t"
-                                     "ds_read_b64 %4, %7 offset:%9\n\t"
-                                     "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
-                                     : "=&s"(ex), "+v"(alo[0]), "+v"(alo[1]), "+v"(ahi[0]), "+v"(ahi[1])
-                                     : "s"(mlo), "s"(mhi), "v"(xa), "i"(PO * p), "i"(PO * p + 128)
-                                     : "memory", "scc");
-                    }
-#pragma unroll
-                    for (int jr = 0; jr < AJ; jr++) {
-                        const int j = j0 + jr;
-                        const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-                        const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(f16x8, make_ulonglong2(alo[jr], ahi[jr])), wo[jr], z, 0, 0, 0);
-                        const float sb = dw[jr] * dxs[jr]; // w_scale * d_x, as the reference
-#pragma unroll
-                        for (int jj = 0; jj < 4; jj++) acc[p][pi][jj] = __builtin_fmaf(d[jj], sb, acc[p][pi][jj]);
-                        if (DUMP) {
-                            // the block's int32: the sum of its 8 word dots
-                            int bs = (int)d[0] + (int)d[1] + (int)d[2] + (int)d[3];
-                            bs += __shfl_xor(bs, 16);
-                            int32_t *dump = n < 8 ? a.dump_a : a.dump_b;
-                            const int i = 2 * p + drow;
-                            if (dump && !(kq & 1) && i < cnt)
-                                dump[((size_t)(beg + i) * rows + orow) * NB + 8 * g + pi + 2 * j] = bs;
-                        }
-                    }
-                }
-                // one pair's LDS reads and MFMA results live at a time
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-    };
-    auto step = [&](int h, const typename W::Step &w) {
-        if constexpr (W::BOTH) {
-            compute(h, std::integral_constant<int, 0>(), w);
-            compute(h, std::integral_constant<int, 1>(), w);
-        } else if (h & 1) {
-            compute(h >> 1, std::integral_constant<int, 1>(), w);
-        } else {
-            compute(h >> 1, std::integral_constant<int, 0>(), w);
-        }
-    };
-    // two steps per turn, loads one ahead
-    static_assert(W::STEPS % 2 == 0, "steps");
-    for (int h = 0; h < W::STEPS; h += 2) {
-        wsrc.load(h + 1, w1);
-        step(h, w0);
-        if (h + 2 < W::STEPS) wsrc.load(h + 2, w0);
-        step(h + 1, w1);
-    }
     // Q4_K's mins, per (input row, weight row): the sum over super-blocks
     // and sub-block pairs, in that order, of dmin * (m_a * s_a + m_b * s_b)
     // (the chain kernels' q4k_mins), s the input row's block sums; super-
-    // blocks outermost so that each header is decoded once for all pairs
-    float mins[NPR];
+    // blocks outermost so that each header is decoded once for all rows.
+    // Formed before the chains, while their registers are free.
+    float mins[GNT][4];
 #pragma unroll
-    for (int p = 0; p < NPR; p++) mins[p] = 0.0f;
+    for (int t = 0; t < GNT; t++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) mins[t][q] = 0.0f;
     if constexpr (Q4K) {
-        const int4 *hd = reinterpret_cast<const int4 *>((n < 8 ? M.s : B.s) + wr * (K / 256) * 16);
+        const int4 *hd = reinterpret_cast<const int4 *>((li < 16 ? M.s : B.s) + wr * (K / 256) * 16);
+#pragma unroll 1
         for (int sbk = 0; sbk < K / 256; sbk++) {
             const int4 h = hd[sbk];
             const float dmin = f16_to_f32((uint32_t)h.x >> 16);
@@ -792,39 +682,209 @@ __global__ __launch_bounds__(QNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
                 mf[sb] = (float)(sb < 4 ? byte_at4(h, 4 + sb + 4) & 63
                                         : (byte_at4(h, 4 + sb + 4) >> 4) | ((byte_at4(h, 4 + sb) >> 6) << 4));
 #pragma unroll
-            for (int p = 0; p < NPR; p++) {
-                if (2 * p < cnt) {
-                    const float *sr = xs_s + (2 * p + drow) * DSTR;
+            for (int t = 0; t < GNT; t++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float *sr = xs_s + (8 * t + 2 * q + kg) * SSTR;
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const int s2 = 4 * sbk + j;
-                        mins[p] = mins[p] + dmin * (mf[2 * j] * sr[lay::q8_scale(K, 2 * s2)] +
-                                                    mf[2 * j + 1] * sr[lay::q8_scale(K, 2 * s2 + 1)]);
+                        mins[t][q] = mins[t][q] + dmin * (mf[2 * j] * sr[lay::q8_scale(K, 2 * s2)] +
+                                                          mf[2 * j + 1] * sr[lay::q8_scale(K, 2 * s2 + 1)]);
                     }
                 }
-            }
         }
     }
-    // the reference's tree: u_l = chain (0, l) + chain (1, l); v = u_l +
-    // u_(l+4) (the lane with kq ^ 1 holds words 4..7); (v0 + v2) + (v1 + v3);
-    // Q4_K then subtracts its mins; then silu(gate) * up, up from column n + 8
-    const bool store = n < 8 && !(kq & 1);
+    // The A operand: A row li = 4 t + w keeps word 4 hh + w of input row t,
+    // which lane kg = w / 2 holds in its low half (w even) or high half (w
+    // odd); every other half of every lane is zero.  The registers start at
+    // zero and the lanes load only their own half (reads under an exec mask,
+    // ANDed with the current exec), so the zeros stay and no lane reads LDS
+    // for them.
+    const int at = li >> 2, aw = li & 3;
+    const bool mine = (aw >> 1) == kg;
+    const uint64_t mlo = __ballot(mine && !(aw & 1)), mhi = __ballot(mine && (aw & 1));
+    const uint32_t xa0 = (uint32_t)reinterpret_cast<uintptr_t>(xop_s + at * XRS + aw);
+    constexpr int TO = 8 * XRS * 8; // bytes from tile to tile
+    static_assert(TO * (GNT - 1) + 32 < 65536, "ds_read offsets are 16-bit");
+    static_assert(GNT == 2, "two tiles");
+    // The chains and everything after, for NT 8-row tiles: a slot of at most
+    // 8 pairs takes one tile (no MFMAs or FMAs for rows that do not exist).
+    auto run = [&](auto nt_c) {
+        constexpr int NT = decltype(nt_c)::value;
+        constexpr int NM = 2 * NT; // MFMAs per block: (half, tile), half-major
+        uint64_t alo[NM], ahi[NM];
 #pragma unroll
-    for (int p = 0; p < NPR; p++) {
-        if (2 * p < cnt) {
-            float v[4];
+        for (int i = 0; i < NM; i++) alo[i] = ahi[i] = 0ull;
+        // chains acc[tile][q][pi][l] of input row 8 tile + 2 q + kg, weight row li
+        float acc[NT][4][2][8];
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const float uu = acc[p][0][jj] + acc[p][1][jj];
-                v[jj] = uu + __shfl_xor(uu, 16);
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int pi = 0; pi < 2; pi++)
+#pragma unroll
+                    for (int l = 0; l < 8; l++) acc[t][q][pi][l] = 0.0f;
+        // the blocks 8 g + pi + 2 j, j = 0..3, of parity pi (a compile-time
+        // constant: it picks the chain accumulators)
+        auto compute = [&](int g, auto pi_c, const typename W::Step &w) {
+            constexpr int pi = decltype(pi_c)::value;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int b = 8 * g + pi + 2 * j;
+                // w_scale * d_x of each of the lane's input rows, as the reference
+                const float dw = W::scale(w, pi, j);
+                const int sidx = lay::q8_scale(K, b);
+                float sb[NT][4];
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const float4 dx = *reinterpret_cast<const float4 *>(xd_s + sidx * DSTR + t * 8 + kg * 4);
+                    sb[t][0] = dw * dx.x;
+                    sb[t][1] = dw * dx.y;
+                    sb[t][2] = dw * dx.z;
+                    sb[t][3] = dw * dx.w;
+                }
+                // A: both halves of each tile, low words under one mask, high
+                // under the other, exec restored, then a wait for them (in
+                // the same statement: the compiler takes an asm's outputs as
+                // ready when it ends, and may copy them right after)
+                const uint32_t xa = xa0 + b * 64;
+                uint64_t ex;
+                if constexpr (NT == 2) {
+                    asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %9, %0\n\t"
+                                 "ds_read_b64 %1, %11\n\t"
+                                 "ds_read_b64 %2, %11 offset:%12\n\t"
+                                 "ds_read_b64 %3, %11 offset:32\n\t"
+                                 "ds_read_b64 %4, %11 offset:%13\n\t"
+                                 "s_and_b64 exec, %10, %0\n\t"
+                                 "ds_read_b64 %5, %11\n\t"
+                                 "ds_read_b64 %6, %11 offset:%12\n\t"
+                                 "ds_read_b64 %7, %11 offset:32\n\t"
+                                 "ds_read_b64 %8, %11 offset:%13\n\t"
+                                 "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
+                                 : "=&s"(ex), "+v"(alo[0]), "+v"(alo[1]), "+v"(alo[2]), "+v"(alo[3]),
+                                   "+v"(ahi[0]), "+v"(ahi[1]), "+v"(ahi[2]), "+v"(ahi[3])
+                                 : "s"(mlo), "s"(mhi), "v"(xa), "i"(TO), "i"(TO + 32)
+                                 : "memory", "scc");
+                } else {
+                    asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %5, %0\n\t"
+                                 "ds_read_b64 %1, %7\n\t"
+                                 "ds_read_b64 %2, %7 offset:32\n\t"
+                                 "s_and_b64 exec, %6, %0\n\t"
+                                 "ds_read_b64 %3, %7\n\t"
+                                 "ds_read_b64 %4, %7 offset:32\n\t"
+                                 "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
+                                 : "=&s"(ex), "+v"(alo[0]), "+v"(alo[1]), "+v"(ahi[0]), "+v"(ahi[1])
+                                 : "s"(mlo), "s"(mhi), "v"(xa)
+                                 : "memory", "scc");
+                }
+                auto mfma = [&](int m, const f16x8 &wo) {
+                    const f32x16 z = {};
+                    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        __builtin_bit_cast(f16x8, make_ulonglong2(alo[m], ahi[m])), wo, z, 0, 0, 0);
+                };
+                int bsum[NT][4];
+                auto chains = [&](int m, const f32x16 &d) {
+                    const int hh = m / NT, t = m % NT;
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++)
+                            acc[t][q][pi][4 * hh + r] = __builtin_fmaf(d[4 * q + r], sb[t][q], acc[t][q][pi][4 * hh + r]);
+                    if (DUMP) {
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const int s4 = (int)d[4 * q] + (int)d[4 * q + 1] + (int)d[4 * q + 2] + (int)d[4 * q + 3];
+                            bsum[t][q] = hh ? bsum[t][q] + s4 : s4;
+                        }
+                    }
+                };
+                // each half's weight operand converted just before its MFMAs;
+                // one MFMA result live at a time (issuing the next MFMA before
+                // the FMAs of the last measured slower)
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    const f16x8 wo = W::operand(w, pi, j, hh);
+#pragma unroll
+                    for (int t = 0; t < NT; t++) {
+                        chains(hh * NT + t, mfma(hh * NT + t, wo));
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (DUMP) {
+                    int32_t *dump = li < 16 ? a.dump_a : a.dump_b;
+#pragma unroll
+                    for (int t = 0; t < NT; t++)
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const int i = 8 * t + 2 * q + kg;
+                            if (dump && i < cnt) dump[((size_t)(beg + i) * rows + orow) * NB + b] = bsum[t][q];
+                        }
+                }
             }
-            float t = (v[0] + v[2]) + (v[1] + v[3]);
-            if constexpr (Q4K) t = t - mins[p];
-            const int i = 2 * p + drow;
-            const float up = __shfl_xor(t, 8);
-            if (store && i < cnt) a.out[(size_t)(beg + i) * rows + orow] = silu_mul_t(t, up, exp_tab);
+        };
+        auto step = [&](int h, const typename W::Step &w) {
+            if constexpr (W::BOTH) {
+                compute(h, std::integral_constant<int, 0>(), w);
+                compute(h, std::integral_constant<int, 1>(), w);
+            } else if (h & 1) {
+                compute(h >> 1, std::integral_constant<int, 1>(), w);
+            } else {
+                compute(h >> 1, std::integral_constant<int, 0>(), w);
+            }
+        };
+        // two steps per turn, loads one ahead (the last turn reloads its own
+        // step rather than branch: a branch in the loop body lets the
+        // compiler sink the chains' FMAs past it, keeping every MFMA result
+        // of a step live at once)
+        static_assert(W::STEPS % 2 == 0, "steps");
+        // step h of parity PAR (compile-time: a runtime parity would be a
+        // branch in the loop body, past which the compiler sinks the chains'
+        // FMAs, keeping every MFMA result of a step live at once)
+        auto stepc = [&](int h, auto par_c, const typename W::Step &w) {
+            if constexpr (W::BOTH) {
+                compute(h, std::integral_constant<int, 0>(), w);
+                compute(h, std::integral_constant<int, 1>(), w);
+            } else {
+                compute(h >> 1, par_c, w);
+            }
+        };
+        // two steps in flight per wave, loads one ahead (a deeper ring, three
+        // steps for Q8_0, measured slower); the last turn reloads its own step
+        // rather than branch
+        typename W::Step w1;
+#pragma unroll 1
+        for (int h = 0; h < W::STEPS; h += 2) {
+            wsrc.load(h + 1, w1);
+            stepc(h, std::integral_constant<int, 0>(), w0);
+            wsrc.load(min(h + 2, W::STEPS - 2), w0);
+            stepc(h + 1, std::integral_constant<int, 1>(), w1);
         }
-    }
+        // the reference's tree, within the lane: u_l = chain (0, l) + chain
+        // (1, l); v_l = u_l + u_(l+4); (v0 + v2) + (v1 + v3); Q4_K then
+        // subtracts its mins; then silu(gate) * up, up from column li + 16
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float v[4];
+#pragma unroll
+                for (int l = 0; l < 4; l++) {
+                    const float u0 = acc[t][q][0][l] + acc[t][q][1][l];
+                    const float u1 = acc[t][q][0][l + 4] + acc[t][q][1][l + 4];
+                    v[l] = u0 + u1;
+                }
+                float s = (v[0] + v[2]) + (v[1] + v[3]);
+                if constexpr (Q4K) s = s - mins[t][q];
+                const float up = __shfl_xor(s, 16);
+                const int i = 8 * t + 2 * q + kg;
+                if (li < 16 && i < cnt) a.out[(size_t)(beg + i) * rows + orow] = silu_mul_t(s, up, exp_tab);
+            }
+    };
+    if (cnt > 8) run(std::integral_constant<int, 2>());
+    else run(std::integral_constant<int, 1>());
 }
 
 
@@ -1107,16 +1167,16 @@ hipError_t launch_gu_t(MvArgs a, int routed, int shared, hipStream_t st)
     a.n_sh = shared ? (a.T + a.sh_chunk - 1) / a.sh_chunk : 0;
     const int slots = a.u_max + a.n_sh;
     if (slots == 0) return hipSuccess;
-    if (a.sh_chunk > QT || M.rows % (QW * 8)) return hipErrorInvalidValue;
-    a.n_rt = M.rows / (QW * 8);
+    if (a.sh_chunk > QT || M.rows % G_ROWS_WG) return hipErrorInvalidValue;
+    a.n_rt = M.rows / G_ROWS_WG;
     const dim3 grid((unsigned)((slots + N_XCD - 1) / N_XCD * N_XCD * a.n_rt));
     const bool dump = a.dump_a || a.dump_b;
 #define BIV_GU_CASE(TY, KK)                                                                                     \
     if (M.ty == TY && M.cols == KK) {                                                                           \
         if (dump)                                                                                               \
-            k_gu_exact<TY, KK, true><<<grid, QNTH, 0, st>>>(a);                                                 \
+            k_gu_exact<TY, KK, true><<<grid, GNTH, 0, st>>>(a);                                                 \
         else                                                                                                    \
-            k_gu_exact<TY, KK, false><<<grid, QNTH, 0, st>>>(a);                                                \
+            k_gu_exact<TY, KK, false><<<grid, GNTH, 0, st>>>(a);                                                \
         return hipGetLastError();                                                                               \
     }
     BIV_GU_CASE(T_Q8_0, 2048)
