@@ -68,6 +68,28 @@ BIV_EXPF_QUAL float biv_expf_finish(float x, double r, uint64_t ki, uint64_t ent
     return (float)y;
 }
 
+/* biv_expf_finish with no early return: the polynomial is evaluated for
+ * every x and the special cases are selected after, so a caller's table
+ * read is never behind a branch.  Same bits as biv_expf_finish. */
+BIV_EXPF_QUAL float biv_expf_finish_sel(float x, double r, uint64_t ki, uint64_t entry)
+{
+    const double c0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
+    const double c1 = 0x1.ebfce50fac4f3p-3 / (32.0 * 32.0);
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    uint64_t t = entry + (ki << 47);
+    double s;
+    memcpy(&s, &t, 8);
+    const double zz = c0 * r + c1;
+    const double r2 = r * r;
+    double y = c2 * r + 1.0;
+    y = zz * r2 + y;
+    y = y * s;
+    float res = (float)y;
+    res = x < -0x1.9fe368p6f ? 0.0f : res;
+    res = x > 0x1.62e42ep6f ? x * 0x1p127f * 0x1p127f : res;
+    return x != x ? x + x : res;
+}
+
 BIV_EXPF_QUAL float biv_expf_ref(float x)
 {
     static const uint64_t tab[32] = BIV_EXPF_TAB_INIT;

@@ -24,6 +24,18 @@ __device__ inline int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(
 // f32::exp of the reference: glibc's expf, restated bit for bit (expf_ref.h)
 __device__ inline float exp_f32(float x) { return biv_expf_ref(x); }
 
+// glibc's expf table (expf_ref.h) in global memory, for kernels that copy it
+// into LDS first: exp_lds then costs one LDS read, where exp_f32 costs a
+// dependent global (L2) load
+__device__ const uint64_t exp_tab_g[32] = BIV_EXPF_TAB_INIT;
+__device__ inline float exp_lds(float x, const uint64_t *tab)
+{
+    double r;
+    uint64_t ki;
+    const uint32_t i = biv_expf_reduce(x, &r, &ki);
+    return biv_expf_finish_sel(x, r, ki, tab[i]);
+}
+
 // ops::sigmoid (ops.rs:159-162)
 __device__ inline float sigmoid(float x) { return 1.0f / (1.0f + exp_f32(-x)); }
 
@@ -537,11 +549,24 @@ __device__ inline void topk_lists(const unsigned (&key)[MAX_EXPERTS_PER_LANE], u
     lst[3] = a3;
 #pragma unroll
     for (int i = 4; i < TOPK_FAST; i++) lst[i] = 0u;
+    // six levels; each lane meets a partner holding a list of other keys:
+    // within a row of 16 lanes by DPP (quad_perm [1,0,3,2], [2,3,0,1], then
+    // row_ror 4 and 8: after the second level a lane group of four is
+    // uniform, and rotating by one group, then by two, meets disjoint groups),
+    // then lanes 16 and 32 apart
 #pragma unroll
-    for (int off = 1; off < WAVE; off <<= 1) {
+    for (int lvl = 0; lvl < 6; lvl++) {
         unsigned m[TOPK_FAST];
 #pragma unroll
-        for (int i = 0; i < TOPK_FAST; i++) m[i] = (unsigned)__shfl_xor((int)lst[TOPK_FAST - 1 - i], off);
+        for (int i = 0; i < TOPK_FAST; i++) {
+            const int v = (int)lst[TOPK_FAST - 1 - i];
+            m[i] = (unsigned)(lvl == 0   ? __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false)
+                              : lvl == 1 ? __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false)
+                              : lvl == 2 ? __builtin_amdgcn_mov_dpp(v, 0x124, 0xF, 0xF, false)
+                              : lvl == 3 ? __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false)
+                              : lvl == 4 ? __shfl_xor(v, 16)
+                                         : __shfl_xor(v, 32));
+        }
         // the top half of a bitonic merge of two descending lists, then the
         // half-cleaners that sort that bitonic sequence
 #pragma unroll
@@ -563,45 +588,63 @@ __device__ inline void topk_lists(const unsigned (&key)[MAX_EXPERTS_PER_LANE], u
 // ids/wts and, when given, to the LDS copies lds_ids/lds_wts.
 constexpr int RPER = MAX_EXPERTS_PER_LANE;
 
-__device__ void route_token(const float *__restrict__ logits, int n_expert, int k, int t, float *es,
-                            int *__restrict__ ids, float *__restrict__ wts, int *lds_ids, float *lds_wts)
+// LDS writes of this wavefront visible to all its lanes
+__device__ inline void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+
+// token t's logits, RPER per lane (-inf past n_expert)
+__device__ inline void load_logits(const float *__restrict__ logits, int n_expert, int t, float (&v)[RPER])
 {
     const int lane = threadIdx.x & 63;
-    float v[RPER];
-    float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < RPER; j++) {
         const int i = lane + WAVE * j;
         v[j] = i < n_expert ? logits[(size_t)t * n_expert + i] : -INFINITY;
-        mx = fmaxf(mx, v[j]);
     }
+}
+
+// v: the token's logits (load_logits); tab: the exp table in LDS
+__device__ void route_token(float (&v)[RPER], const uint64_t *tab, int n_expert, int k, int t, float *es,
+                            int *__restrict__ ids, float *__restrict__ wts, int *lds_ids, float *lds_wts)
+{
+    const int lane = threadIdx.x & 63;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < RPER; j++) mx = fmaxf(mx, v[j]);
     if (mx != mx) mx = -INFINITY; // f32::max skips NaN
     mx = ordered_to_f32(wave_max_u32(f32_to_ordered(mx)));
 #pragma unroll
     for (int j = 0; j < RPER; j++) {
         const int i = lane + WAVE * j;
-        v[j] = i < n_expert ? exp_f32(v[j] - mx) : 0.0f;
+        const float ev = exp_lds(v[j] - mx, tab); // every lane: no branch around the table read
+        v[j] = i < n_expert ? ev : 0.0f;
         es[i] = v[j]; // zeros past n_expert: adding +0 leaves the positive sum's bits alone
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     // the sum in index order, as the reference's loop adds it: one chain, the
-    // same in every lane; reads issued 16 values ahead of the adds
+    // same in every lane; the reads well ahead of the adds
     float sum = 0.0f;
     const float4 *e4 = reinterpret_cast<const float4 *>(es);
     constexpr int NQ = MAX_EXPERTS_PER_LANE * WAVE / 4;
+    // 12 reads (48 values) kept in flight ahead of the adds: the chain,
+    // not the LDS latency, sets the pace
+    constexpr int LA = 12;
+    float4 q[NQ];
 #pragma unroll
-    for (int i0 = 0; i0 < NQ; i0 += 4) {
-        float4 q[4];
+    for (int i = 0; i < LA; i++) q[i] = e4[i];
 #pragma unroll
-        for (int u = 0; u < 4; u++) q[u] = e4[i0 + u];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            sum = sum + q[u].x;
-            sum = sum + q[u].y;
-            sum = sum + q[u].z;
-            sum = sum + q[u].w;
-        }
+    for (int i = 0; i < NQ; i++) {
+        if (i + LA < NQ) q[i + LA] = e4[i + LA];
+        sum = sum + q[i].x;
+        sum = sum + q[i].y;
+        sum = sum + q[i].z;
+        sum = sum + q[i].w;
     }
     const float inv = 1.0f / sum;
     // probabilities as keys: bits + 1 orders like the float (p >= 0), 0 once taken
@@ -618,11 +661,50 @@ __device__ void route_token(const float *__restrict__ logits, int n_expert, int 
         // skipping those equal keys already ranked (lower index first).
         unsigned lst[TOPK_FAST];
         topk_lists(key, lst);
+        // Every lane holds the same list.  Without equal keys among the k
+        // largest (nor between the k-th and the next), exactly k keys are at
+        // least the k-th, and each one's rank is the number of listed keys
+        // above it: those lanes write their experts to LDS by rank (es is
+        // free again: the sum has read it).  Equal keys take the ballot
+        // walk below, which breaks ties by the lower index.
+        unsigned kth = lst[0];
+#pragma unroll
+        for (int r = 1; r < TOPK_FAST; r++) kth = r == k - 1 ? lst[r] : kth;
+        int ncand = 0;
+#pragma unroll
+        for (int j = 0; j < RPER; j++) ncand += __popcll(__ballot(key[j] >= kth));
+        bool ties = ncand != k;
+#pragma unroll
+        for (int r = 0; r + 1 < TOPK_FAST; r++) ties |= r + 1 < k && lst[r] == lst[r + 1];
+        if (!ties) {
+            int *sel = reinterpret_cast<int *>(es);
+#pragma unroll
+            for (int j = 0; j < RPER; j++) {
+                if (key[j] >= kth) {
+                    int rank = 0;
+#pragma unroll
+                    for (int r = 0; r < TOPK_FAST; r++) rank += r < k && lst[r] > key[j];
+                    sel[rank] = lane + WAVE * j;
+                }
+            }
+            wave_lds_sync();
+            // weights' numerators and their sum in rank order (the
+            // reference's iterator sum)
+#pragma unroll
+            for (int r = 0; r < TOPK_FAST; r++) {
+                if (r >= k) break;
+                const float bp = __uint_as_float(lst[r] - 1u);
+                if (r == lane) sel_p = bp;
+                s += bp;
+            }
+            if (lane < k) sel_i = sel[lane];
+        }
         // every lane holds the same list: scalar values from here on
         unsigned prev = 0u;
         int before = 0; // earlier ranks holding the current key
 #pragma unroll
         for (int r = 0; r < TOPK_FAST; r++) {
+            if (!ties) break; // uniform
             if (r >= k) break;
             const unsigned kr = (unsigned)__builtin_amdgcn_readfirstlane((int)lst[r]);
             before = r > 0 && prev == kr ? before + 1 : 0;
@@ -717,13 +799,6 @@ __device__ void route_token(const float *__restrict__ logits, int n_expert, int 
 constexpr int MAX_EXPERTS = 256;
 constexpr int RS_THREADS = 1024;
 
-// LDS writes of this wavefront visible to all its lanes
-__device__ inline void wave_lds_sync()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // The same dispatch as sort_pairs for P <= 4 * WAVE pairs, by one wavefront
 // and without workgroup barriers.  A pair's place among its expert's pairs is
@@ -799,6 +874,63 @@ __device__ void sort_pairs_wave(const int *ids, const float *wts, int n_expert, 
         dp.tok_pairs[(size_t)t * k + rank] = p;
         if (r % chunk < SLOT_TOKS) dp.slots[sfirst[e] + r / chunk].tok[r % chunk] = t;
     }
+}
+
+// The same dispatch for P <= WAVE pairs with every expert's pairs in one
+// slot (T <= chunk), by one wavefront with no per-expert arrays: lane i takes
+// pair i and counts, over all pairs j, those of a lower expert, those of its
+// expert from earlier tokens (a token names an expert once) and those of its
+// own token with a lower expert.  Its dispatch position is the first two
+// counts, the first count its expert's first position; a first pair marks
+// that position, and the marks below it, as a ballot, number the expert's
+// slot.  mark is an LDS array of WAVE ints.
+#ifndef BIV_SMALL_SORT_P
+#define BIV_SMALL_SORT_P 16 // pairs up to which the route takes sort_pairs_small (measured: faster up to T = 2)
+#endif
+__device__ void sort_pairs_small(const int *ids, const float *wts, int k, int T, const Dispatch &dp, int *mark)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int P = T * k;
+    const bool act = lane < P;
+    const int e = act ? ids[lane] : 0x7FFFFFFF;
+    const int t = lane / k, t0 = t * k;
+    int lt = 0, eqb = 0, eqt = 0, rk = 0;
+    // every id first (P is a multiple of 4 here), then the counts
+    int4 q[WAVE / 4];
+#pragma unroll
+    for (int r = 0; r < WAVE / 4; r++)
+        if (4 * r < P) q[r] = *reinterpret_cast<const int4 *>(ids + 4 * r); // uniform
+#pragma unroll
+    for (int r = 0; r < WAVE / 4; r++) {
+        if (4 * r >= P) break; // uniform
+        const int ej[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int j = 4 * r + u;
+            const bool below = ej[u] < e, eq = ej[u] == e;
+            lt += below;
+            eqt += eq;
+            eqb += eq && j < t0;
+            rk += below && j >= t0 && j < t0 + k;
+        }
+    }
+    const int pos = lt + eqb;
+    mark[lane] = 0;
+    wave_lds_sync();
+    if (act && eqb == 0) mark[pos] = 1;
+    wave_lds_sync();
+    const unsigned long long firsts = __ballot(mark[lane] != 0);
+    const int n_used = __popcll(firsts);
+    if (act) {
+        const int slot = __popcll(firsts & ((1ull << lt) - 1ull)); // lt: the expert's first position
+        dp.pair_tok[pos] = t;
+        dp.pair_exp[pos] = e;
+        dp.pair_w[pos] = wts[lane];
+        dp.tok_pairs[t0 + rk] = pos;
+        if (eqb == 0) reinterpret_cast<int4 *>(&dp.slots[slot])[0] = make_int4(e, pos, eqt, 0);
+        if (eqb < SLOT_TOKS) dp.slots[slot].tok[eqb] = t;
+    }
+    for (int u = n_used + lane; u < dp.slot_cap; u += WAVE) reinterpret_cast<int4 *>(&dp.slots[u])[0] = make_int4(0, 0, 0, 0);
 }
 
 // The counting sort past one workgroup (the `routed` lists of
@@ -931,18 +1063,31 @@ __global__ __launch_bounds__(RS_THREADS) void k_route_sort(const float *__restri
                                                            int T, int chunk, Dispatch dp, int *work)
 {
     __shared__ float es[RS_WAVES][MAX_EXPERTS];
-    __shared__ int lds_ids[RS_WAVES * 16];
+    __shared__ __align__(16) int lds_ids[RS_WAVES * 16];
     __shared__ float lds_wts[RS_WAVES * 16];
     const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const bool single = gridDim.x == 1;
-    for (int t = blockIdx.x * nw + wave; t < T; t += gridDim.x * nw)
-        route_token(logits, n_expert, k, t, es[wave], dp.ids, dp.wts, single ? lds_ids : nullptr,
+    // the first token's logits and the exp table go out together
+    __shared__ uint64_t tab[32];
+    const int t0 = blockIdx.x * nw + wave;
+    float lg[RPER];
+    if (t0 < T) load_logits(logits, n_expert, t0, lg);
+    if (threadIdx.x < 32) tab[threadIdx.x] = exp_tab_g[threadIdx.x];
+    __syncthreads();
+    for (int t = t0; t < T; t += gridDim.x * nw) {
+        if (t != t0) load_logits(logits, n_expert, t, lg);
+        route_token(lg, tab, n_expert, k, t, es[wave], dp.ids, dp.wts, single ? lds_ids : nullptr,
                     single ? lds_wts : nullptr);
+    }
     if (single) {
         // the routes from LDS, sorted by one wavefront
         __shared__ int cnt[2 * MAX_EXPERTS], first[MAX_EXPERTS], sfirst[MAX_EXPERTS]; // cnt: later a u64 bitmap
         __syncthreads();
-        if (wave == 0) sort_pairs_wave(lds_ids, lds_wts, n_expert, k, T, chunk, dp, cnt, first, sfirst);
+        if (wave == 0) {
+            if (T * k <= BIV_SMALL_SORT_P && (T * k) % 4 == 0 && T <= chunk)
+                sort_pairs_small(lds_ids, lds_wts, k, T, dp, cnt);
+            else sort_pairs_wave(lds_ids, lds_wts, n_expert, k, T, chunk, dp, cnt, first, sfirst);
+        }
         return;
     }
     if (single) return;
