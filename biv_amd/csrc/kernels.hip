@@ -1975,6 +1975,20 @@ __global__ __launch_bounds__(DC_WAVES *WAVE) void k_down_combine(DcArgs a)
     Chain<TY, K> wc[DC_D];
 #pragma unroll
     for (int d = 0; d < DC_D; d++) load_unit(wc[d], grp + d * NG);
+    // the combine's operands, fetched now so that none is a dependent load
+    // at the end: the tokens' dispatch positions (their weights once the
+    // staging is done), the shared-expert logits, the residual, exp's table
+    __shared__ uint64_t tab[32];
+    __shared__ int cpos[16 * 16];
+    __shared__ float cwt[16 * 16], csig[16];
+    const int nc = T * k; // <= 256: T <= 16, k <= 16
+    const int cp = tid < nc ? a.dp.tok_pairs[tid] : 0;
+    const float cg = has_shared && tid < T ? a.glogit[tid] : 0.0f;
+    const int ct = tid / DC_RB, cr = tid - ct * DC_RB;
+    const bool cmine = tid < T * DC_RB;
+    float *const cpo = a.out + (size_t)ct * rows + row0 + cr;
+    const float cres = a.add && cmine ? *cpo : 0.0f;
+    if (tid < 32) tab[tid] = exp_tab_g[tid];
     // the intermediate, quantised into LDS: one 32-element block per thread and turn
     for (int b = tid; b < R * (K / 32); b += NTH) {
         const int r = b / (K / 32), bb = b - r * (K / 32);
@@ -1984,6 +1998,7 @@ __global__ __launch_bounds__(DC_WAVES *WAVE) void k_down_combine(DcArgs a)
                        reinterpret_cast<float *>(&stage[r * ROW16 + K / 16]), nullptr);
     }
     __syncthreads();
+    const float cw = tid < nc ? a.dp.pair_w[cp] : 0.0f; // consumed after the rows
     for (int i0 = 0; i0 < per; i0 += DC_D) {
 #pragma unroll
         for (int d = 0; d < DC_D; d++) {
@@ -2025,18 +2040,22 @@ __global__ __launch_bounds__(DC_WAVES *WAVE) void k_down_combine(DcArgs a)
             load_unit(wc[d], v + DC_D * NG);
         }
     }
+    if (tid < nc) {
+        cpos[tid] = cp;
+        cwt[tid] = cw;
+    }
+    if (has_shared && tid < T) csig[tid] = 1.0f / (1.0f + exp_lds(-cg, tab)); // ops::sigmoid
     __syncthreads();
-    // the combine of this workgroup's rows
-    for (int i = tid; i < T * DC_RB; i += NTH) {
-        const int t = i / DC_RB, r = i - t * DC_RB;
+    // the combine of this workgroup's rows: fma(w, y, o) over the token's
+    // experts in ascending id, then the gated shared row (axpy, model.rs:880-895)
+    if (cmine) {
         float o = 0.0f;
         for (int j = 0; j < k; j++) {
-            const int p = a.dp.tok_pairs[(size_t)t * k + j];
-            o = fmaf(a.dp.pair_w[p], ylds[p * DC_RB + r], o);
+            const int p = cpos[ct * k + j];
+            o = fmaf(cwt[ct * k + j], ylds[p * DC_RB + cr], o);
         }
-        if (has_shared) o = fmaf(sigmoid(a.glogit[t]), ylds[(P + t) * DC_RB + r], o);
-        float *po = a.out + (size_t)t * rows + row0 + r;
-        *po = a.add ? *po + o : o;
+        if (has_shared) o = fmaf(csig[ct], ylds[(P + ct) * DC_RB + cr], o);
+        *cpo = a.add ? cres + o : o;
     }
 }
 
