@@ -630,6 +630,13 @@ typedef struct {
     OrcWeight sh_gate, sh_up, sh_down, gate_inp; /* when n_ff_sh > 0 */
 } OrcMoe;
 
+/* Kernel level for the gate and up matmuls of dense_ffn, -1 (default) for the
+ * caller's.  Test-only knob: the scalar level sums each row's block dots in a
+ * different order from the x86 kernels, which measures how far a GPU kernel
+ * summing in its own order would land from the reference's output. */
+static int gu_level = -1;
+void orc_set_gu_level(int level) { gu_level = level; }
+
 /* down(silu(gate x) * up x) of n rows; out is [n x e] */
 int orc_dense_ffn(int gty, const uint8_t *gate, int uty, const uint8_t *up, int dty, const uint8_t *down,
                   size_t e, size_t ff, const float *x, size_t n, float *out, int threads, int level)
@@ -637,8 +644,9 @@ int orc_dense_ffn(int gty, const uint8_t *gate, int uty, const uint8_t *up, int 
     float *g = malloc(sizeof(float) * n * ff), *u = malloc(sizeof(float) * n * ff);
     int rc = -2;
     if (g && u) {
-        rc = orc_matmul(gty, gate, e, ff, x, n, g, threads, level);
-        if (!rc) rc = orc_matmul(uty, up, e, ff, x, n, u, threads, level);
+        const int gl = gu_level >= 0 ? gu_level : level;
+        rc = orc_matmul(gty, gate, e, ff, x, n, g, threads, gl);
+        if (!rc) rc = orc_matmul(uty, up, e, ff, x, n, u, threads, gl);
         if (!rc) {
             for (size_t i = 0; i < n * ff; i++) g[i] = orc_silu(g[i]) * u[i];
             rc = orc_matmul(dty, down, ff, e, g, n, out, threads, level);

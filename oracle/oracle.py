@@ -89,6 +89,7 @@ def lib():
                                     ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
         L.orc_moe.argtypes = [ctypes.POINTER(OrcMoe), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
                               ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        L.orc_set_gu_level.argtypes = [ctypes.c_int]
         L.orc_detect_level.restype = ctypes.c_int
         L.orc_max_threads.restype = ctypes.c_int
         _lib = L
@@ -97,6 +98,11 @@ def lib():
 
 def _p(a):
     return None if a is None else a.ctypes.data
+
+
+def set_gu_level(level):
+    """Kernel level of dense_ffn's gate/up matmuls (-1: the caller's); test only."""
+    lib().orc_set_gu_level(level)
 
 
 def detect_level():
