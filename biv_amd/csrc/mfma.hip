@@ -504,6 +504,9 @@ constexpr int GW = 4;               // waves of a workgroup
 constexpr int GNTH = GW * 64;
 constexpr int G_ROWS_WG = GW * 16;  // output rows of a workgroup
 constexpr int GNT = QT / 8;         // 8-row tiles of a slot
+#ifndef GU_AJ
+#define GU_AJ 2 // blocks per masked A read group
+#endif
 
 // Weight operands of the exact kernel.  A step covers the blocks 8 g + pi +
 // 2 j (j = 0..3) of one parity (Q8_0: a half-group) or both parities (Q4_K:
@@ -706,16 +709,16 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
     const uint64_t mlo = __ballot(mine && !(aw & 1)), mhi = __ballot(mine && (aw & 1));
     const uint32_t xa0 = (uint32_t)reinterpret_cast<uintptr_t>(xop_s + at * XRS + aw);
     constexpr int TO = 8 * XRS * 8; // bytes from tile to tile
-    static_assert(TO * (GNT - 1) + 32 < 65536, "ds_read offsets are 16-bit");
+    static_assert(TO * (GNT - 1) + 160 < 65536, "ds_read offsets are 16-bit");
     static_assert(GNT == 2, "two tiles");
     // The chains and everything after, for NT 8-row tiles: a slot of at most
     // 8 pairs takes one tile (no MFMAs or FMAs for rows that do not exist).
     auto run = [&](auto nt_c) {
         constexpr int NT = decltype(nt_c)::value;
         constexpr int NM = 2 * NT; // MFMAs per block: (half, tile), half-major
-        uint64_t alo[NM], ahi[NM];
+        uint64_t alo[GU_AJ * NM], ahi[GU_AJ * NM]; // [block of the read group][half][tile]
 #pragma unroll
-        for (int i = 0; i < NM; i++) alo[i] = ahi[i] = 0ull;
+        for (int i = 0; i < GU_AJ * NM; i++) alo[i] = ahi[i] = 0ull;
         // chains acc[tile][q][pi][l] of input row 8 tile + 2 q + kg, weight row li
         float acc[NT][4][2][8];
 #pragma unroll
@@ -733,6 +736,87 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int b = 8 * g + pi + 2 * j;
+                // A: both halves of each tile of GU_AJ blocks (this one and
+                // the next ones of the parity, 128 bytes apart), low words
+                // under one mask, high under the other, exec restored, then a
+                // wait for them (in the same statement: the compiler takes an
+                // asm's outputs as ready when it ends, and may copy them
+                // right after)
+                if (j % GU_AJ == 0) {
+                    const uint32_t xa = xa0 + b * 64;
+                    uint64_t ex;
+                    if constexpr (NT == 2 && GU_AJ == 2) {
+                        asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %17, %0\n\t"
+                                     "ds_read_b64 %1, %19\n\t"
+                                     "ds_read_b64 %2, %19 offset:%20\n\t"
+                                     "ds_read_b64 %3, %19 offset:32\n\t"
+                                     "ds_read_b64 %4, %19 offset:%21\n\t"
+                                     "ds_read_b64 %5, %19 offset:128\n\t"
+                                     "ds_read_b64 %6, %19 offset:%22\n\t"
+                                     "ds_read_b64 %7, %19 offset:160\n\t"
+                                     "ds_read_b64 %8, %19 offset:%23\n\t"
+                                     "s_and_b64 exec, %18, %0\n\t"
+                                     "ds_read_b64 %9, %19\n\t"
+                                     "ds_read_b64 %10, %19 offset:%20\n\t"
+                                     "ds_read_b64 %11, %19 offset:32\n\t"
+                                     "ds_read_b64 %12, %19 offset:%21\n\t"
+                                     "ds_read_b64 %13, %19 offset:128\n\t"
+                                     "ds_read_b64 %14, %19 offset:%22\n\t"
+                                     "ds_read_b64 %15, %19 offset:160\n\t"
+                                     "ds_read_b64 %16, %19 offset:%23\n\t"
+                                     "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
+                                     : "=&s"(ex), "+v"(alo[0]), "+v"(alo[1]), "+v"(alo[2]), "+v"(alo[3]),
+                                       "+v"(alo[4]), "+v"(alo[5]), "+v"(alo[6]), "+v"(alo[7]), "+v"(ahi[0]),
+                                       "+v"(ahi[1]), "+v"(ahi[2]), "+v"(ahi[3]), "+v"(ahi[4]), "+v"(ahi[5]),
+                                       "+v"(ahi[6]), "+v"(ahi[7])
+                                     : "s"(mlo), "s"(mhi), "v"(xa), "i"(TO), "i"(TO + 32), "i"(TO + 128),
+                                       "i"(TO + 160)
+                                     : "memory", "scc");
+                    } else if constexpr (NT == 2) {
+                        asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %9, %0\n\t"
+                                     "ds_read_b64 %1, %11\n\t"
+                                     "ds_read_b64 %2, %11 offset:%12\n\t"
+                                     "ds_read_b64 %3, %11 offset:32\n\t"
+                                     "ds_read_b64 %4, %11 offset:%13\n\t"
+                                     "s_and_b64 exec, %10, %0\n\t"
+                                     "ds_read_b64 %5, %11\n\t"
+                                     "ds_read_b64 %6, %11 offset:%12\n\t"
+                                     "ds_read_b64 %7, %11 offset:32\n\t"
+                                     "ds_read_b64 %8, %11 offset:%13\n\t"
+                                     "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
+                                     : "=&s"(ex), "+v"(alo[0]), "+v"(alo[1]), "+v"(alo[2]), "+v"(alo[3]),
+                                       "+v"(ahi[0]), "+v"(ahi[1]), "+v"(ahi[2]), "+v"(ahi[3])
+                                     : "s"(mlo), "s"(mhi), "v"(xa), "i"(TO), "i"(TO + 32)
+                                     : "memory", "scc");
+                    } else if constexpr (GU_AJ == 2) {
+                        asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %9, %0\n\t"
+                                     "ds_read_b64 %1, %11\n\t"
+                                     "ds_read_b64 %2, %11 offset:32\n\t"
+                                     "ds_read_b64 %3, %11 offset:128\n\t"
+                                     "ds_read_b64 %4, %11 offset:160\n\t"
+                                     "s_and_b64 exec, %10, %0\n\t"
+                                     "ds_read_b64 %5, %11\n\t"
+                                     "ds_read_b64 %6, %11 offset:32\n\t"
+                                     "ds_read_b64 %7, %11 offset:128\n\t"
+                                     "ds_read_b64 %8, %11 offset:160\n\t"
+                                     "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
+                                     : "=&s"(ex), "+v"(alo[0]), "+v"(alo[1]), "+v"(alo[2]), "+v"(alo[3]),
+                                       "+v"(ahi[0]), "+v"(ahi[1]), "+v"(ahi[2]), "+v"(ahi[3])
+                                     : "s"(mlo), "s"(mhi), "v"(xa)
+                                     : "memory", "scc");
+                    } else {
+                        asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %5, %0\n\t"
+                                     "ds_read_b64 %1, %7\n\t"
+                                     "ds_read_b64 %2, %7 offset:32\n\t"
+                                     "s_and_b64 exec, %6, %0\n\t"
+                                     "ds_read_b64 %3, %7\n\t"
+                                     "ds_read_b64 %4, %7 offset:32\n\t"
+                                     "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
+                                     : "=&s"(ex), "+v"(alo[0]), "+v"(alo[1]), "+v"(ahi[0]), "+v"(ahi[1])
+                                     : "s"(mlo), "s"(mhi), "v"(xa)
+                                     : "memory", "scc");
+                    }
+                }
                 // w_scale * d_x of each of the lane's input rows, as the reference
                 const float dw = W::scale(w, pi, j);
                 const int sidx = lay::q8_scale(K, b);
@@ -745,44 +829,11 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
                     sb[t][2] = dw * dx.z;
                     sb[t][3] = dw * dx.w;
                 }
-                // A: both halves of each tile, low words under one mask, high
-                // under the other, exec restored, then a wait for them (in
-                // the same statement: the compiler takes an asm's outputs as
-                // ready when it ends, and may copy them right after)
-                const uint32_t xa = xa0 + b * 64;
-                uint64_t ex;
-                if constexpr (NT == 2) {
-                    asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %9, %0\n\t"
-                                 "ds_read_b64 %1, %11\n\t"
-                                 "ds_read_b64 %2, %11 offset:%12\n\t"
-                                 "ds_read_b64 %3, %11 offset:32\n\t"
-                                 "ds_read_b64 %4, %11 offset:%13\n\t"
-                                 "s_and_b64 exec, %10, %0\n\t"
-                                 "ds_read_b64 %5, %11\n\t"
-                                 "ds_read_b64 %6, %11 offset:%12\n\t"
-                                 "ds_read_b64 %7, %11 offset:32\n\t"
-                                 "ds_read_b64 %8, %11 offset:%13\n\t"
-                                 "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
-                                 : "=&s"(ex), "+v"(alo[0]), "+v"(alo[1]), "+v"(alo[2]), "+v"(alo[3]),
-                                   "+v"(ahi[0]), "+v"(ahi[1]), "+v"(ahi[2]), "+v"(ahi[3])
-                                 : "s"(mlo), "s"(mhi), "v"(xa), "i"(TO), "i"(TO + 32)
-                                 : "memory", "scc");
-                } else {
-                    asm volatile("s_mov_b64 %0, exec\n\ts_and_b64 exec, %5, %0\n\t"
-                                 "ds_read_b64 %1, %7\n\t"
-                                 "ds_read_b64 %2, %7 offset:32\n\t"
-                                 "s_and_b64 exec, %6, %0\n\t"
-                                 "ds_read_b64 %3, %7\n\t"
-                                 "ds_read_b64 %4, %7 offset:32\n\t"
-                                 "s_mov_b64 exec, %0\n\ts_waitcnt lgkmcnt(0)"
-                                 : "=&s"(ex), "+v"(alo[0]), "+v"(alo[1]), "+v"(ahi[0]), "+v"(ahi[1])
-                                 : "s"(mlo), "s"(mhi), "v"(xa)
-                                 : "memory", "scc");
-                }
+                const int jo = (j % GU_AJ) * NM; // this block's A operands
                 auto mfma = [&](int m, const f16x8 &wo) {
                     const f32x16 z = {};
                     return __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                        __builtin_bit_cast(f16x8, make_ulonglong2(alo[m], ahi[m])), wo, z, 0, 0, 0);
+                        __builtin_bit_cast(f16x8, make_ulonglong2(alo[jo + m], ahi[jo + m])), wo, z, 0, 0, 0);
                 };
                 int bsum[NT][4];
                 auto chains = [&](int m, const f32x16 &d) {
