@@ -197,6 +197,7 @@ int upload_mat_impl(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n
     case BIV_GGML_Q8_0: qrow = cols; srow = cols / 32 * 2; break;
     case BIV_GGML_Q4_K: qrow = cols / 2; srow = cols / 256 * 16; break;
     case BIV_GGML_Q6_K: qrow = cols / 256 * 192; srow = cols / 256 * 16; drow = cols / 256 * 2; break;
+    case BIV_GGML_F32: qrow = row_bytes; srow = row_bytes; break; // chain layout + row-major copy
     default: qrow = row_bytes; break;
     }
     // the chain layouts (layout.hpp) need whole groups of blocks per row
@@ -256,6 +257,7 @@ int upload_mat_impl(biv_hip_ctx *ctx, int ty, size_t cols, size_t rows, size_t n
             case BIV_GGML_F32:
                 for (int e2 = 0; e2 < K; e2++)
                     memcpy(qd + 4 * biv::lay::f32_elem(e2 / 32, e2 % 32), src + 4 * e2, 4);
+                memcpy(sd, src, row_bytes);
                 break;
             case BIV_GGML_BF16: {
                 // element 128 g + 16 m + L goes to (16 g + L) * 8 + m (lay::bf16_elem)
@@ -562,7 +564,9 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
 
     biv::RouterArgs ra{};
     ra.router = reinterpret_cast<const float *>(m->router->m.q);
+    ra.router_rm = reinterpret_cast<const float *>(m->router->m.s);
     ra.gate_inp = has_shared ? reinterpret_cast<const float *>(m->gi->m.q) : nullptr;
+    ra.gate_rm = has_shared ? reinterpret_cast<const float *>(m->gi->m.s) : nullptr;
     ra.n_expert = ne;
     ra.E = E;
     ra.T = T;

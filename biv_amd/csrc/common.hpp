@@ -26,7 +26,7 @@ struct DevMat {
     int ty = -1;
     int cols = 0, rows = 0, n = 0;
     uint8_t *q = nullptr;
-    uint8_t *s = nullptr;
+    uint8_t *s = nullptr; // F32: the rows as given (row-major), besides q's chain layout
     uint8_t *d = nullptr;
 };
 
@@ -64,7 +64,9 @@ struct Dispatch {
 
 struct RouterArgs {
     const float *router;   // [n_expert][E], f32 chain layout
+    const float *router_rm; // the same rows row-major (the matrix-core router at prefill)
     const float *gate_inp; // [E] or nullptr
+    const float *gate_rm;  // the same row as given (row-major)
     int n_expert, E, T;
     const float *h;        // [T][E]
     float *logits;         // [T][n_expert]

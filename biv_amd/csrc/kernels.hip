@@ -103,13 +103,14 @@ __device__ inline void quant_block_at(const float (&v)[32], int K, int b, int *q
 }
 
 // The same from a block in LDS, read twice (amax, then the quants) so that
-// few registers are live.
-__device__ inline void quant_block_lds(const float4 *v, int K, int b, int *qrow, float *drow)
+// few registers are live; 16-byte word l of the block at v[l ^ sw].
+__device__ inline void quant_block_lds(const float4 *v, int K, int b, int *qrow, float *drow, float *srow = nullptr,
+                                       int sw = 0)
 {
     float amax = 0.0f;
 #pragma unroll
     for (int q = 0; q < 8; q++) {
-        const float4 f = v[q];
+        const float4 f = v[q ^ sw];
         amax = fmaxf(amax, fabsf(f.x));
         amax = fmaxf(amax, fabsf(f.y));
         amax = fmaxf(amax, fabsf(f.z));
@@ -117,15 +118,22 @@ __device__ inline void quant_block_lds(const float4 *v, int K, int b, int *qrow,
     }
     const float db = amax / 127.0f;
     const float id = db != 0.0f ? 1.0f / db : 0.0f;
+    int sum = 0;
 #pragma unroll
     for (int l = 0; l < 8; l++) {
-        const float4 f = v[l];
-        const unsigned w = ((unsigned)((int)roundf(f.x * id)) & 0xFF) | (((unsigned)((int)roundf(f.y * id)) & 0xFF) << 8) |
-                           (((unsigned)((int)roundf(f.z * id)) & 0xFF) << 16) |
-                           (((unsigned)((int)roundf(f.w * id)) & 0xFF) << 24);
+        const float4 f = v[l ^ sw];
+        const int r0 = (int)roundf(f.x * id), r1 = (int)roundf(f.y * id), r2 = (int)roundf(f.z * id),
+                  r3 = (int)roundf(f.w * id);
+        sum += r0;
+        sum += r1;
+        sum += r2;
+        sum += r3;
+        const unsigned w = ((unsigned)r0 & 0xFF) | (((unsigned)r1 & 0xFF) << 8) | (((unsigned)r2 & 0xFF) << 16) |
+                           (((unsigned)r3 & 0xFF) << 24);
         qrow[lay::q8_word(b, l)] = (int)w;
     }
     drow[lay::q8_scale(K, b)] = db;
+    if (srow) srow[lay::q8_scale(K, b)] = db * (float)sum;
 }
 
 __device__ inline void quant_block(const float (&v)[32], int K, size_t row, int b, int8_t *qs, float *d, float *s)
@@ -322,125 +330,210 @@ template <int NS, int TC, int NTH = 256> __global__ __launch_bounds__(NTH) void 
     }
 }
 
-// The router at prefill sizes, register-blocked: each 32-lane half wave runs
-// chain L of dot_f32 for RB rows x 8 tokens (8 RB accumulators), so a value
-// read from LDS feeds several FMAs rather than one.  A workgroup (8 half
-// waves) takes 2 RB rows x 32 tokens.  Both operands go straight from global memory into LDS,
-// RT_KC steps of 32 elements at a time: the router
-// rows as stored (f32 chain layout: lane L's four steps in one 16-byte word),
-// the tokens row-major (lane L reads element 32 s + L, conflict-free), into
-// two buffers, one stage ahead of the compute.  Per (row, token) every FMA is the
-// reference's, in its order, then the same tree: the logits carry k_router's
-// bits.
-// RB rows per half wave: 8 (16-row tiles) for long chunks; 4 (8-row tiles,
-// twice the workgroups) up to BIV_RT_RB4_T tokens, where 16-row tiles leave
-// about one wave per SIMD.
-constexpr int RT_TOKS = 32, RT_KC = 4; // RT_KC steps of 32 elements per stage
 #ifndef BIV_RT_MIN_T
 #define BIV_RT_MIN_T 256
 #endif
-constexpr int RT_MIN_T = BIV_RT_MIN_T; // tokens from which launch_router takes it
-#ifndef BIV_RT_RB4_T
-#define BIV_RT_RB4_T 512
+constexpr int RT_MIN_T = BIV_RT_MIN_T; // tokens from which launch_router takes the matrix-core router
+// tokens from which it takes 32-row tiles of 32 tokens, of 64 tokens
+#ifndef BIV_RM_M_T
+#define BIV_RM_M_T 1024
+#endif
+#ifndef BIV_RM_L_T
+#define BIV_RM_L_T 2048
 #endif
 
-template <int RB> __global__ __launch_bounds__(256) void k_router_tiled(RouterArgs a, int n_tr, int n_tt)
+// The router at prefill sizes on the matrix cores.  v_mfma_f32_*x1f32 (one
+// product per output, k = 1) rounds each output exactly as fmaf does, so a
+// block of it is one FMA step of one chain of dot_f32 (quant.rs:1177-1207)
+// for a whole tile of (row, token) pairs: chain L's accumulator for (r, t)
+// takes w[r][32 s + L] * h[t][32 s + L] at step s = 0, 1, ..., in the
+// reference's order, and the tree (quant.rs:1149-1153) follows at the end.
+//
+// Both operands are staged row-major (the router's row-major copy), so one
+// 16-byte LDS read gives chains 4 c .. 4 c + 3 at one step: component m feeds
+// the m-th MFMA of the step.  Each MFMA's two chain blocks (lanes of cs = 0
+// and 1) take chains L and L + 8, which the tree adds first, so that level
+// is an add within the lane; a wave's chain group c is one of 0, 1, 4, 5.
+// Eight waves: four chain groups times two (halves of m when MI = 2, two
+// 32-token sub-tiles when MI = 4).  SH = 32: v_mfma_f32_32x32x1f32, a
+// 32-row x 32-token block; SH = 16: v_mfma_f32_16x16x1f32 with blocks
+// (chain, 16-token group), a 16-row x 32-token block.
+//
+// A stage is 4 steps (128 elements) of the tile's rows and tokens, NB stages
+// in flight.  The gate logit and the Q8 of h come from k_prep, before.
+typedef float f32x32_t __attribute__((ext_vector_type(32)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+template <int SH> struct RmAcc;
+template <> struct RmAcc<32> {
+    using T = f32x32_t;
+    static __device__ T step(float x, float y, T c) { return __builtin_amdgcn_mfma_f32_32x32x1f32(x, y, c, 0, 0, 0); }
+};
+template <> struct RmAcc<16> {
+    using T = f32x16_t;
+    static __device__ T step(float x, float y, T c) { return __builtin_amdgcn_mfma_f32_16x16x1f32(x, y, c, 0, 0, 0); }
+};
+
+constexpr int RM_NTH = 512;
+template <int SH, int MI> constexpr int rm_tokens() { return 32 * (MI / 2); }
+template <int SH, int MI> constexpr int rm_nbuf() { return SH == 32 && MI == 4 ? 3 : 4; }
+
+// s_waitcnt for at most N vector memory operations outstanding (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left free)
+template <int N> __device__ inline void wait_vm()
 {
-    constexpr int RT_ROWS = 2 * RB;
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// stage st of a thread's NLD words: word q * RM_NTH + tid lands at that
+// index of the buffer (global_load_lds writes a wave's 64 words in lane
+// order); the first NW are router words (offsets from wb), the rest token
+// words (from xb)
+// One 16-byte-per-lane global -> LDS load (LDS address m0 + 16 lane), in
+// inline asm: the compiler, which cannot tell which stage buffer an LDS DMA
+// writes, would otherwise wait for every DMA in flight before each LDS read
+// and undo the prefetch.  The caller waits for it with wait_vm.  (Writing m0
+// needs one wait state before the DMA reads it.)
+__device__ inline void lds_dma16(const float *g, const float4 *lds_dst)
+{
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(
+        (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)lds_dst);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+}
+
+template <int NLD, int NW>
+__device__ inline void rm_issue(const float *wb, const float *xb, const unsigned (&off)[NLD], int st, float4 *base, int w)
+{
+#pragma unroll
+    for (int q = 0; q < NLD; q++) lds_dma16((q < NW ? wb : xb) + off[q] + 128 * st, base + q * RM_NTH + w * WAVE);
+}
+
+// a workgroup barrier with no memory fence: the stage loop orders its LDS
+// itself (its loads' waits), and a fence would also wait for the stores in flight
+__device__ inline void rm_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// slot of a workgroup's tile: the tiles are dealt round-robin over the 8
+// XCDs by workgroup id, so give XCD x a run of consecutive tiles (row tiles
+// fastest): the row tiles of one token tile then share that XCD's L2
+__device__ inline int rm_tile(int b, int n)
+{
+    const int q = n >> 3, r = n & 7, x = b & 7, i = b >> 3;
+    return x * q + min(x, r) + i;
+}
+
+template <int SH, int MI> __global__ __launch_bounds__(RM_NTH) void k_router_mfma(RouterArgs a, int n_tr, int n_tt)
+{
+    constexpr int RT = SH, TT = rm_tokens<SH, MI>(), NB = rm_nbuf<SH, MI>();
+    constexpr int WORDS = (RT + TT) * 32; // 16-byte words of one stage
+    constexpr int NLD = WORDS / RM_NTH;   // words each thread stages
+    constexpr int NW = RT * 32 / RM_NTH;  // of them router words
+    constexpr int EP = 32 * (RT + 1);     // floats of one chain plane of the epilogue (padded)
+    constexpr int STAGE_W = NB * WORDS, EPI_W = 16 * EP / 4;
+    static_assert(NLD * RM_NTH == WORDS && NW * RM_NTH == RT * 32, "whole stages");
+    __shared__ float4 lds[STAGE_W > EPI_W ? STAGE_W : EPI_W];
     const int E = a.E, ne = a.n_expert, T = a.T, tid = threadIdx.x;
-    const int tile = blockIdx.x;
-    if (tile >= n_tr * n_tt) {
-        // the Q8 of h for the experts, in the workgroups past the tiles
-        const int nq = gridDim.x - n_tr * n_tt;
-        for (int i = (tile - n_tr * n_tt) * 256 + tid; i < T * (E / 32); i += nq * 256) {
-            float v[32];
-            load32(a.h + 32 * (size_t)i, v);
-            quant_block(v, E, i / (E / 32), i % (E / 32), a.xq, a.xd, a.xs);
-        }
-        return;
-    }
-    // row tiles fastest, so that consecutive workgroups share a token tile
+    const int tile = rm_tile(blockIdx.x, n_tr * n_tt);
     const int tr = tile % n_tr, tt = tile / n_tr;
-    const int r0 = tr * RT_ROWS, t0 = tt * RT_TOKS;
-    constexpr int WP = RT_KC / 4 * 32;       // 16-byte words of a router row's stage
-    constexpr int XP = RT_KC * 32 / 4;       // 16-byte words of a token's stage
-    constexpr int NW = RT_ROWS * WP / 256;   // words per thread
-    constexpr int NX = RT_TOKS * XP / 256;
-    static_assert(NW * 256 == RT_ROWS * WP && NX * 256 == RT_TOKS * XP, "whole waves of 16-byte words");
-    __shared__ float4 Wl[2][RT_ROWS * WP];
-    __shared__ float4 Xl[2][RT_TOKS * XP];
-    const int lane = tid & 31, hw = tid >> 5, rg = hw & 1, tg = hw >> 1, wv = tid >> 6;
-    auto lds = [](const void *src, float4 *dst_wave) {
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst_wave, 16, 0, 0);
-    };
-    auto issue = [&](int c) {
-        const int b = c & 1;
+    const int r0 = tr * RT, t0 = tt * TT;
+    const int lane = tid & 63, w = tid >> 6, cg = w & 3, ws = w >> 2;
+    const int c = (cg & 1) | ((cg >> 1) << 2); // chains 4 c .. 4 c + 3 and 4 c + 8 ..
+    const int sp = MI == 4 ? ws : 0;           // token sub-tile
+    const int m0 = MI == 4 ? 0 : 2 * ws;       // first of the MI steps' components
+    // this lane's operand rows: A row ar of the tile, B token bt of the sub-tile
+    const int cs = SH == 32 ? lane >> 5 : (lane >> 4) & 1;
+    const int ar = SH == 32 ? (lane & 31) : (lane & 15);
+    const int bt = SH == 32 ? (lane & 31) : (lane & 15) + 16 * (lane >> 5);
+    const int wd = c ^ (2 * cs);
+    // a stage row (RT router rows, then TT tokens) holds 32 words, word x at
+    // x ^ (row & 15), which spreads a column of rows over the banks
+    const int arow = ar, brow = RT + 32 * sp + bt;
+    unsigned off[NLD];
 #pragma unroll
-        for (int q = 0; q < NW; q++) {
-            const int i = q * 256 + tid, r = i / WP, f = i - r * WP, row = r0 + r;
-            const float *w = row < ne ? a.router + (size_t)row * E : (row == ne && a.gate_inp ? a.gate_inp : a.router);
-            lds(reinterpret_cast<const float4 *>(w) + (size_t)c * WP + f, &Wl[b][q * 256 + wv * WAVE]);
+    for (int q = 0; q < NLD; q++) {
+        const int g = q * RM_NTH + tid, row = g >> 5, word = (g & 31) ^ (row & 15);
+        off[q] = q < NW ? (unsigned)(min(r0 + row, ne - 1) * E + 4 * word)
+                        : (unsigned)((size_t)min(t0 + row - RT, T - 1) * E + 4 * word);
+    }
+    using Acc = typename RmAcc<SH>::T;
+    Acc acc[MI];
+#pragma unroll
+    for (int m = 0; m < MI; m++)
+#pragma unroll
+        for (int k = 0; k < (int)(sizeof(Acc) / 4); k++) acc[m][k] = 0.0f;
+    const int nst = E / 128;
+    for (int p = 0; p < NB - 1 && p < nst; p++) rm_issue<NLD, NW>(a.router_rm, a.h, off, p, lds + p * WORDS, w);
+    for (int st = 0; st < nst; st++) {
+        // this stage's words; the later stages' loads stay in flight
+        const int ahead = min(nst - 1 - st, NB - 2);
+        if (NB > 3 && ahead >= 2) wait_vm<2 * NLD>();
+        else if (ahead >= 1) wait_vm<NLD>();
+        else wait_vm<0>();
+        rm_barrier();
+        if (st + NB - 1 < nst) rm_issue<NLD, NW>(a.router_rm, a.h, off, st + NB - 1, lds + ((st + NB - 1) % NB) * WORDS, w);
+        const float4 *base = lds + (st % NB) * WORDS;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int x = 8 * k + wd;
+            if constexpr (MI == 4) {
+                const float4 A = base[arow * 32 + (x ^ (arow & 15))];
+                const float4 B = base[brow * 32 + (x ^ (brow & 15))];
+                acc[0] = RmAcc<SH>::step(A.x, B.x, acc[0]);
+                acc[1] = RmAcc<SH>::step(A.y, B.y, acc[1]);
+                acc[2] = RmAcc<SH>::step(A.z, B.z, acc[2]);
+                acc[3] = RmAcc<SH>::step(A.w, B.w, acc[3]);
+            } else {
+                const float2 A = reinterpret_cast<const float2 *>(base + arow * 32 + (x ^ (arow & 15)))[ws];
+                const float2 B = reinterpret_cast<const float2 *>(base + brow * 32 + (x ^ (brow & 15)))[ws];
+                acc[0] = RmAcc<SH>::step(A.x, B.x, acc[0]);
+                acc[1] = RmAcc<SH>::step(A.y, B.y, acc[1]);
+            }
         }
+    }
+    // epilogue, one 32-token sub-tile at a time: the chain-L-plus-L+8 sums
+    // (chains L in 0..7, 16..23) to LDS planes [16][token][row], then a
+    // thread per (row, token) finishes the tree: + L ^ 16, ^ 4, ^ 2, ^ 1
+    float *pl = reinterpret_cast<float *>(lds);
+    constexpr int NSUB = MI == 4 ? 2 : 1;
 #pragma unroll
-        for (int q = 0; q < NX; q++) {
-            const int i = q * 256 + tid, t = i / XP, f = i - t * XP, tok = min(t0 + t, T - 1);
-            lds(reinterpret_cast<const float4 *>(a.h + (size_t)tok * E + (size_t)c * RT_KC * 32) + f,
-                &Xl[b][q * 256 + wv * WAVE]);
-        }
-    };
-    float acc[RB][8];
+    for (int sub = 0; sub < NSUB; sub++) {
+        __syncthreads(); // the stages (or the previous sub-tile's planes) are read
+        if (sp == sub) {
 #pragma unroll
-    for (int r = 0; r < RB; r++)
+            for (int m = 0; m < MI; m++) {
+                const int L16 = (c & 1) * 4 + m0 + m + 8 * (c >> 2);
+                float *plane = pl + L16 * EP;
+                if constexpr (SH == 32) {
 #pragma unroll
-        for (int t = 0; t < 8; t++) acc[r][t] = 0.0f;
-    const int nc = E / 32 / RT_KC;
-    // two buffers: chunk c + 1 loads while chunk c computes (three, two
-    // ahead, measured slower: 72 KB of LDS leaves two workgroups per CU)
-    issue(0);
-    for (int c = 0; c < nc; c++) {
-        __builtin_amdgcn_s_waitcnt(0); // this chunk's stage (the only loads in flight)
-        __syncthreads();
-        if (c + 1 < nc) issue(c + 1);
-        const int b = c & 1;
-        const float *xb = reinterpret_cast<const float *>(&Xl[b][0]);
+                    for (int k = 0; k < 16; k++) {
+                        const int i = 8 * (k >> 2) + 4 * (lane >> 5) + (k & 3), j = lane & 31;
+                        plane[j * (RT + 1) + i] = acc[m][k] + acc[m][k + 16];
+                    }
+                } else {
 #pragma unroll
-        for (int s4 = 0; s4 < RT_KC / 4; s4++) {
-            float4 w[RB];
+                    for (int g = 0; g < 2; g++)
 #pragma unroll
-            for (int r = 0; r < RB; r++) w[r] = Wl[b][(rg * RB + r) * WP + s4 * 32 + lane];
-#pragma unroll
-            for (int t = 0; t < 8; t++) {
-                const float *xr = xb + (tg * 8 + t) * (RT_KC * 32) + s4 * 128 + lane;
-                const float x0 = xr[0], x1 = xr[32], x2 = xr[64], x3 = xr[96];
-#pragma unroll
-                for (int r = 0; r < RB; r++) {
-                    float v = acc[r][t];
-                    v = fmaf(w[r].x, x0, v);
-                    v = fmaf(w[r].y, x1, v);
-                    v = fmaf(w[r].z, x2, v);
-                    v = fmaf(w[r].w, x3, v);
-                    acc[r][t] = v;
+                        for (int r = 0; r < 4; r++) {
+                            const int i = 4 * (lane >> 4) + r, j = (lane & 15) + 16 * g;
+                            plane[j * (RT + 1) + i] = acc[m][8 * g + r] + acc[m][8 * g + 4 + r];
+                        }
                 }
             }
         }
-    }
-    const int nrows = ne + (a.gate_inp ? 1 : 0);
+        __syncthreads();
+        for (int o = tid; o < 32 * RT; o += RM_NTH) {
+            const int row = o % RT, tok = o / RT;
+            float p[16];
 #pragma unroll
-    for (int r = 0; r < RB; r++)
+            for (int l = 0; l < 16; l++) p[l] = pl[l * EP + tok * (RT + 1) + row];
+            float s2[8];
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-            float v = acc[r][t];
-            v = v + __shfl_xor(v, 8);  // acc0+acc1 (lanes 0-7), acc2+acc3 (16-23)
-            v = v + __shfl_xor(v, 16); // (acc0+acc1)+(acc2+acc3)
-            v = v + __shfl_xor(v, 4);  // the two 128-bit halves
-            v = v + __shfl_xor(v, 2);  // movehl
-            v = v + __shfl_xor(v, 1);  // movehdup
-            const int row = r0 + rg * RB + r, tok = t0 + tg * 8 + t;
-            if (lane == ((r * 8 + t) & 31) && row < nrows && tok < T) {
-                if (row < ne) a.logits[(size_t)tok * ne + row] = v;
-                else a.glogit[tok] = v;
-            }
+            for (int l = 0; l < 8; l++) s2[l] = p[l] + p[l + 8];
+            const float s30 = s2[0] + s2[4], s31 = s2[1] + s2[5], s32 = s2[2] + s2[6], s33 = s2[3] + s2[7];
+            const float v = (s30 + s32) + (s31 + s33);
+            const int gr = r0 + row, gt = t0 + 32 * sub + tok;
+            if (gr < ne && gt < T) a.logits[(size_t)gt * ne + gr] = v;
         }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -594,6 +687,82 @@ __device__ inline void wave_lds_sync()
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The prefill pre-pass of the matrix-core router, a wave per token:
+//   with norm_w, ops::rms_norm (ops.rs:136-144): ss in dot_f32's 32-chain
+//     order (chain L in lane L, as k_rms_norm), scale, v = x * (scale * w),
+//     written to hn;
+//   the shared expert's gate logit gate_inp . h in dot_f32's order
+//     (quant.rs:1177-1207), chain L in lane L, then the tree;
+//   the Q8 for the experts of the (normalised) row: it goes through LDS
+//     (32-element blocks at a 36-float pitch) so that lane b quantises
+//     block b.
+// Lanes 32-63 repeat the chains of lanes 0-31 (the shuffle tree stays within
+// each half); each half writes half of the row (to hn and LDS).  The norm
+// weights and the gate row, the chains' operands, are staged in LDS once per
+// workgroup.
+constexpr int PREP_TOK = 4, PREP_PITCH = 36; // tokens (waves) per workgroup; LDS floats per block
+template <int NS> __global__ __launch_bounds__(64 * PREP_TOK) void k_prep(RouterArgs a)
+{
+    constexpr int E = 32 * NS;
+    __shared__ __align__(16) float wn[E];
+    __shared__ __align__(16) float wg[E];
+    __shared__ __align__(16) float rows[PREP_TOK][NS * PREP_PITCH];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, L = lane & 31, hi = lane >> 5;
+    const int t = blockIdx.x * PREP_TOK + w;
+    // the weights go straight to LDS (DMA), the token's row to registers;
+    // then all of it is waited for
+    {
+        float4 *wn4 = reinterpret_cast<float4 *>(wn), *wg4 = reinterpret_cast<float4 *>(wg);
+#pragma unroll
+        for (int q = 0; q * 64 * PREP_TOK < E / 4; q++) {
+            const int i0 = q * 64 * PREP_TOK + 64 * w; // this wave's 64 words
+            if (i0 < E / 4) {
+                if (a.norm_w) lds_dma16(a.norm_w + 4 * (i0 + lane), wn4 + i0);
+                if (a.gate_rm) lds_dma16(a.gate_rm + 4 * (i0 + lane), wg4 + i0);
+            }
+        }
+    }
+    const float *g = a.h + (size_t)min(t, a.T - 1) * E;
+    float v[NS];
+#pragma unroll
+    for (int k = 0; k < NS; k++) v[k] = g[L + 32 * k];
+    wait_vm<0>();
+    __syncthreads();
+    if (t >= a.T) return; // uniform over the wave, which syncs only itself from here
+    if (a.norm_w) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NS; k++) acc = fmaf(v[k], v[k], acc);
+        const float scale = rms_scale(acc, E, a.eps);
+        float *o = a.hn + (size_t)t * E;
+#pragma unroll
+        for (int k = 0; k < NS; k++) {
+            v[k] = v[k] * (scale * wn[L + 32 * k]);
+            if ((k < NS / 2) == (hi == 0)) o[L + 32 * k] = v[k];
+        }
+    }
+    if (a.gate_rm) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NS; k++) acc = fmaf(wg[L + 32 * k], v[k], acc);
+        acc = acc + __shfl_xor(acc, 8);
+        acc = acc + __shfl_xor(acc, 16);
+        acc = acc + __shfl_xor(acc, 4);
+        acc = acc + __shfl_xor(acc, 2);
+        acc = acc + __shfl_xor(acc, 1);
+        if (lane == 0) a.glogit[t] = acc;
+    }
+    float *r = &rows[w][0];
+#pragma unroll
+    for (int k = 0; k < NS; k++)
+        if ((k < NS / 2) == (hi == 0)) r[k * PREP_PITCH + L] = v[k];
+    wave_lds_sync();
+    if (lane < NS)
+        quant_block_lds(reinterpret_cast<const float4 *>(r + lane * PREP_PITCH), E, lane,
+                        reinterpret_cast<int *>(a.xq + (size_t)t * E), a.xd + (size_t)t * (E / 32),
+                        a.xs + (size_t)t * (E / 32));
 }
 
 
@@ -2148,19 +2317,25 @@ hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, i
 hipError_t launch_router(const RouterArgs &a0, hipStream_t st)
 {
     RouterArgs a = a0;
-    if (a.norm_w && a.T >= RT_MIN_T) {
-        // the tiled router stages tokens a piece at a time: rms_norm into hn first
-        hipError_t e = launch_rms_norm(a.h, a.hn, a.norm_w, a.T, a.E, a.eps, st);
-        if (e != hipSuccess) return e;
-        a.h = a.hn;
-        a.norm_w = nullptr;
-    }
-    if (a.T >= RT_MIN_T && a.E % (32 * RT_KC) == 0) {
-        const int rows = a.T <= BIV_RT_RB4_T ? 8 : 16;
-        const int n_tr = (a.n_expert + 1 + rows - 1) / rows, n_tt = (a.T + RT_TOKS - 1) / RT_TOKS;
-        const int qblocks = a.T * (a.E / 32), nq = (qblocks + 4 * 256 - 1) / (4 * 256);
-        if (rows == 8) k_router_tiled<4><<<n_tr * n_tt + nq, 256, 0, st>>>(a, n_tr, n_tt);
-        else k_router_tiled<8><<<n_tr * n_tt + nq, 256, 0, st>>>(a, n_tr, n_tt);
+    if (a.T >= RT_MIN_T && a.E % 128 == 0 && a.router_rm && (!a.gate_inp || a.gate_rm)) {
+        // the pre-pass (norm into hn, gate logit, Q8 of h), then the logits of
+        // the (normalised) rows in tiles of 16 x 32 (row x token), 32 x 32 or
+        // 32 x 64: the largest that still gives the chip a few hundred workgroups
+        const int nb = (a.T + PREP_TOK - 1) / PREP_TOK;
+        if (a.E == 2048) k_prep<64><<<nb, 64 * PREP_TOK, 0, st>>>(a);
+        else if (a.E == 1024) k_prep<32><<<nb, 64 * PREP_TOK, 0, st>>>(a);
+        else if (a.E == 512) k_prep<16><<<nb, 64 * PREP_TOK, 0, st>>>(a);
+        else return hipErrorInvalidValue;
+        if (a.norm_w) a.h = a.hn;
+#define BIV_RM_LAUNCH(SH, MI)                                                                              \
+    do {                                                                                                   \
+        const int n_tr = (a.n_expert + SH - 1) / SH, n_tt = (a.T + rm_tokens<SH, MI>() - 1) / rm_tokens<SH, MI>(); \
+        k_router_mfma<SH, MI><<<n_tr * n_tt, RM_NTH, 0, st>>>(a, n_tr, n_tt);                             \
+    } while (0)
+        if (a.T >= BIV_RM_L_T) BIV_RM_LAUNCH(32, 4);
+        else if (a.T >= BIV_RM_M_T) BIV_RM_LAUNCH(32, 2);
+        else BIV_RM_LAUNCH(16, 2);
+#undef BIV_RM_LAUNCH
         return hipGetLastError();
     }
     const int rows = a.n_expert + 1;

@@ -183,6 +183,28 @@ def test_router_ties(orc, engine, groups):
                     assert ids[tok, r] < ids[tok, r + 1]
 
 
+@pytest.mark.parametrize("T,ne,E,shared", [(256, 8, 512, True), (257, 40, 2048, True), (1100, 48, 1024, False),
+                                             (2100, 256, 512, True)])
+def test_router_prefill_tiles(orc, engine, T, ne, E, shared):
+    """The matrix-core router (T >= 256) in each of its tile shapes (16 x 32
+    below 1024 tokens, 32 x 32, 32 x 64 from 2048), with expert counts that
+    leave a row tile part-filled, token counts that leave the last token tile
+    part-filled, with and without the shared expert's gate logit: logits and
+    gate logit bit-identical to the oracle's dot_f32 of the same rows."""
+    print(f"case router tiles T={T} ne={ne} E={E} shared={shared}", flush=True)
+    layer, moe = layer_for(engine, seed=71, n_embd=E, n_expert=ne, k=min(8, ne), shared=shared)
+    h = synth.make_tokens(900 + T, T, n_embd=E, offsets=True)
+    _, t = moe.ffn_taps(h, dots=False)
+    if orc.detect_level() < orc.AVX2:
+        pytest.skip("the oracle's dot_f32 order needs AVX2 on the host")
+    want = orc.matmul(synth.F32, layer.router.data, E, ne, h, threads=8)
+    bad = np.argwhere(t["logits"].view(np.uint32) != want.view(np.uint32))
+    assert bad.size == 0, f"{len(bad)} logits differ, first (token, expert) {bad[:4].tolist()}"
+    if shared:
+        g = orc.matmul(synth.F32, layer.shared[3].data, E, 1, h, threads=8)[:, 0]
+        assert np.array_equal(t["shared_logit"].view(np.uint32), g.view(np.uint32)), "gate logits differ"
+
+
 @pytest.mark.parametrize("T", [1, 5, 17, 63])
 def test_bf16_layer(orc, engine, T):
     """BF16 experts (config 4) below the matrix-core size: f32 activations,
