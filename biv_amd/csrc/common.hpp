@@ -35,7 +35,8 @@ struct DevMat {
 // of its first SLOT_TOKS pairs (entries past cnt are not written).
 constexpr int SLOT_TOKS = 8;
 struct alignas(16) Slot {
-    int expert, beg, cnt, pad; // cnt 0: an unused slot
+    int expert, beg, cnt; // cnt 0: an unused slot
+    int used;             // the number of slots in use (in every used record; 0 in unused ones)
     int tok[SLOT_TOKS];
 };
 

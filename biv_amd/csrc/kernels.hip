@@ -1015,7 +1015,7 @@ __device__ void sort_pairs_wave(const int *ids, const float *wts, int n_expert, 
             sfirst[e] = spos;
             for (int q = 0; q < ns[j]; q++)
                 reinterpret_cast<int4 *>(&dp.slots[spos + q])[0] =
-                    make_int4(e, pos + q * chunk, min(chunk, c[j] - q * chunk), 0);
+                    make_int4(e, pos + q * chunk, min(chunk, c[j] - q * chunk), n_used);
         }
         pos += c[j];
         spos += ns[j];
@@ -1096,7 +1096,7 @@ __device__ void sort_pairs_small(const int *ids, const float *wts, int k, int T,
         dp.pair_exp[pos] = e;
         dp.pair_w[pos] = wts[lane];
         dp.tok_pairs[t0 + rk] = pos;
-        if (eqb == 0) reinterpret_cast<int4 *>(&dp.slots[slot])[0] = make_int4(e, pos, eqt, 0);
+        if (eqb == 0) reinterpret_cast<int4 *>(&dp.slots[slot])[0] = make_int4(e, pos, eqt, n_used);
         if (eqb < SLOT_TOKS) dp.slots[slot].tok[eqb] = t;
     }
     for (int u = n_used + lane; u < dp.slot_cap; u += WAVE) reinterpret_cast<int4 *>(&dp.slots[u])[0] = make_int4(0, 0, 0, 0);
@@ -1195,7 +1195,8 @@ __global__ __launch_bounds__(MAX_EXPERTS *DS_SPLIT) void k_dispatch_scan(int n_e
     work[(size_t)nb * MAX_EXPERTS + e] = first;
     work[(size_t)(nb + 1) * MAX_EXPERTS + e] = sfirst;
     for (int j = 0; j < nsl; j++)
-        reinterpret_cast<int4 *>(&dp.slots[sfirst + j])[0] = make_int4(e, first + j * chunk, min(chunk, tot - j * chunk), 0);
+        reinterpret_cast<int4 *>(&dp.slots[sfirst + j])[0] =
+            make_int4(e, first + j * chunk, min(chunk, tot - j * chunk), n_used);
     for (int u = n_used + e; u < dp.slot_cap; u += MAX_EXPERTS) reinterpret_cast<int4 *>(&dp.slots[u])[0] = make_int4(0, 0, 0, 0);
 }
 

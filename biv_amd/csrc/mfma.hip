@@ -25,6 +25,37 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int WAVE = 64;
+constexpr int N_XCD = 8;
+
+// (slot, row tile) of workgroup b of a grouped launch.  The units (the
+// shared expert's slots, then the routed slots in use, row tiles fastest)
+// go to the 8 XCDs in runs of RUN slots, run g to XCD g % 8 (workgroup
+// ids go round-robin over the XCDs): an expert's consecutive slots, and
+// every row tile of a slot, then share one XCD's L2, so that the expert's
+// rows come from HBM about once, while runs from all over the dispatch
+// order keep the XCDs' loads alike.  (Slots of the BF16 kernel hold up to
+// 256 pairs, one expert each as a rule: runs of 1.)  The routed slots in
+// use are counted in every used slot record.  False: no unit for this
+// workgroup.
+constexpr int SLOT_RUN = 4, SLOT_RUN_BF16 = 1;
+template <int RUN, class Args> __device__ inline bool slot_unit(const Args &a, int b, int &u, int &rt)
+{
+    const int used = a.u_max > 0 ? min(a.dp.slots[0].used, a.u_max) : 0;
+    const int n = (a.n_sh + used) * a.n_rt, run = RUN * a.n_rt;
+    const int x = b % N_XCD, i = b / N_XCD;
+    const int unit = (x + N_XCD * (i / run)) * run + i % run;
+    if (unit >= n) return false;
+    u = unit / a.n_rt;
+    rt = unit % a.n_rt;
+    return true;
+}
+// workgroups of a grouped launch over `slots` slots (an upper bound) of
+// n_rt row tiles: every XCD's share of the runs
+template <int RUN> inline unsigned slot_grid(int slots, int n_rt)
+{
+    const int runs = (slots + RUN - 1) / RUN;
+    return (unsigned)(N_XCD * ((runs + N_XCD - 1) / N_XCD) * RUN * n_rt);
+}
 
 __device__ inline uint32_t bf16_bits(float x)
 {
@@ -95,7 +126,6 @@ constexpr int NWR = 2;              // waves along the rows
 constexpr int TOK_TILE = 64 * NWT;  // pairs of a workgroup
 constexpr int NTH = 64 * NWT * NWR; // threads of a workgroup
 constexpr int SK = 4;               // chunks per stage
-constexpr int N_XCD = 8;
 static_assert(TOK_TILE == MFMA_TOK_TILE, "slot size");
 
 template <int K, bool GATEUP>
@@ -115,9 +145,8 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     // the two waves of a SIMD (waves w and w + 4) take pairs 64 apart x 2
     const int wt = wave >> 1, wr = wave & 1;
     // workgroup -> (slot, row tile): ids b with one b % 8 are one XCD's
-    const int G = N_XCD * a.n_rt, b = blockIdx.x;
-    const int u = (b / G) * N_XCD + b % N_XCD, rt = (b % G) / N_XCD;
-    if (u >= a.u_max + a.n_sh) return;
+    int u, rt;
+    if (!slot_unit<SLOT_RUN_BF16>(a, blockIdx.x, u, rt)) return;
     const bool shared = u < a.n_sh;
     int e = 0, beg, cnt, tok0 = 0;
     if (shared) {
@@ -337,9 +366,8 @@ __global__ __launch_bounds__(QNTH) void k_q8_down_mfma(MvArgs a)
     __shared__ float xd_s[NB * DSTR];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, kq = lane >> 4;
-    const int G = N_XCD * a.n_rt, bid = blockIdx.x;
-    const int u = (bid / G) * N_XCD + bid % N_XCD, rt = (bid % G) / N_XCD;
-    if (u >= a.u_max + a.n_sh) return;
+    int u, rt;
+    if (!slot_unit<SLOT_RUN>(a, blockIdx.x, u, rt)) return;
     const bool shared = u < a.n_sh;
     int e = 0, beg, cnt;
     if (shared) {
@@ -614,9 +642,8 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
     __shared__ float xs_s[Q4K ? QT * SSTR : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 31, kg = lane >> 5;
-    const int G = N_XCD * a.n_rt, bid = blockIdx.x;
-    const int u = (bid / G) * N_XCD + bid % N_XCD, rt = (bid % G) / N_XCD;
-    if (u >= a.u_max + a.n_sh) return;
+    int u, rt;
+    if (!slot_unit<SLOT_RUN>(a, blockIdx.x, u, rt)) return;
     const bool shared = u < a.n_sh;
     int e = 0, beg, cnt, tok0 = 0;
     if (shared) {
@@ -970,9 +997,8 @@ __global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
     __shared__ float xd_s[NB * DSTR];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, kq = lane >> 4;
-    const int G = N_XCD * a.n_rt, bid = blockIdx.x;
-    const int u = (bid / G) * N_XCD + bid % N_XCD, rt = (bid % G) / N_XCD;
-    if (u >= a.u_max + a.n_sh) return;
+    int u, rt;
+    if (!slot_unit<SLOT_RUN>(a, blockIdx.x, u, rt)) return;
     const bool shared = u < a.n_sh;
     int e = 0, beg, cnt;
     if (shared) {
@@ -1131,7 +1157,7 @@ template <bool GATEUP> hipError_t launch_mfma_t(MfArgs a, int routed, int shared
     if (M.rows % row_tile) return hipErrorInvalidValue;
     if (a.chunk > TOK_TILE || a.sh_chunk > TOK_TILE) return hipErrorInvalidValue;
     a.n_rt = M.rows / row_tile;
-    const dim3 grid((unsigned)((slots + N_XCD - 1) / N_XCD * N_XCD * a.n_rt));
+    const dim3 grid(slot_grid<SLOT_RUN_BF16>(slots, a.n_rt));
 #define BIV_MF_CASE(KK)                                                                                         \
     if (M.cols == KK) {                                                                                         \
         k_mfma_bf16<KK, GATEUP><<<grid, NTH, 0, st>>>(a);                                                       \
@@ -1168,7 +1194,7 @@ hipError_t launch_q8_down_t(MvArgs a, int routed, int shared, hipStream_t st)
     if (slots == 0) return hipSuccess;
     if (a.sh_chunk > QT || M.rows % Q_ROWS_WG) return hipErrorInvalidValue;
     a.n_rt = M.rows / Q_ROWS_WG;
-    const dim3 grid((unsigned)((slots + N_XCD - 1) / N_XCD * N_XCD * a.n_rt));
+    const dim3 grid(slot_grid<SLOT_RUN>(slots, a.n_rt));
 #define BIV_Q8_CASE(KK)                                                                                         \
     if (M.cols == KK) {                                                                                         \
         if (a.dump_a)                                                                                           \
@@ -1220,7 +1246,7 @@ hipError_t launch_gu_t(MvArgs a, int routed, int shared, hipStream_t st)
     if (slots == 0) return hipSuccess;
     if (a.sh_chunk > QT || M.rows % G_ROWS_WG) return hipErrorInvalidValue;
     a.n_rt = M.rows / G_ROWS_WG;
-    const dim3 grid((unsigned)((slots + N_XCD - 1) / N_XCD * N_XCD * a.n_rt));
+    const dim3 grid(slot_grid<SLOT_RUN>(slots, a.n_rt));
     const bool dump = a.dump_a || a.dump_b;
 #define BIV_GU_CASE(TY, KK)                                                                                     \
     if (M.ty == TY && M.cols == KK) {                                                                           \
