@@ -108,10 +108,9 @@ __device__ inline float silu_mul_t(float g, float u, const uint64_t *tab)
 // gate/up: each block has a gate and an up accumulator and the SwiGLU is
 // formed in the epilogue.
 //
-// The row tiles of a slot go to one XCD (workgroup ids b, b + 8, ... are
-// dispatched to one XCD): the slot's activation rows come from HBM once per
-// slot and from that XCD's L2 after, and every expert's weights are read
-// once per slot.
+// The row tiles of a slot go to one XCD (slot_unit): the slot's activation
+// rows come from HBM once per slot and from that XCD's L2 after, and every
+// expert's weights are read once per slot.
 //
 // K advances in stages of 32 (4 chunks, 64 bytes of a row).  A stage's tiles
 // go straight from global memory into LDS (global_load_lds) into a ring of
