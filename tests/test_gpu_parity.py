@@ -74,6 +74,31 @@ def check_block_dots(orc, layer, h, t):
         assert np.array_equal(t["down_idots"][p], orc.block_idots_rows(dty, dw, E, t["act_q"][p])), ("down", p)
 
 
+def check_block_dots_sampled(orc, layer, h, t, n_pairs, seed, extra=()):
+    """check_block_dots on a seeded sample of the pairs (and shared rows),
+    plus the rows `extra`: prefill sizes have too many for the oracle to redo
+    them all."""
+    T, k, E, ff = h.shape[0], layer.k, layer.n_embd, layer.n_ff
+    P = T * k
+    R = P + (T if layer.shared is not None else 0)
+    rng = np.random.default_rng(seed)
+    rows = sorted(set(rng.choice(R, size=min(n_pairs, R), replace=False).tolist()) | set(extra))
+    print(f"block dots of {len(rows)} of {R} rows", flush=True)
+    for p in rows:
+        if p < P:
+            e, tok = int(t["pair_expert"][p]), int(t["pair_token"][p])
+            gw, uw, dw = layer.gate.expert(e), layer.up.expert(e), layer.down.expert(e)
+            gty, uty, dty = layer.gate.ty, layer.up.ty, layer.down.ty
+        else:
+            tok = p - P
+            sg, su, sd, _ = layer.shared
+            gw, uw, dw, gty, uty, dty = sg.data, su.data, sd.data, sg.ty, su.ty, sd.ty
+        xq = orc.q8act(h[tok])[0]
+        assert np.array_equal(t["gate_idots"][p], orc.block_idots_rows(gty, gw, ff, xq)), ("gate", p)
+        assert np.array_equal(t["up_idots"][p], orc.block_idots_rows(uty, uw, ff, xq)), ("up", p)
+        assert np.array_equal(t["down_idots"][p], orc.block_idots_rows(dty, dw, E, t["act_q"][p])), ("down", p)
+
+
 def check_dispatch(t, ids, T, k):
     """Dispatch order: pairs grouped by ascending expert, tokens ascending
     within an expert, exactly the pairs the routing chose."""
@@ -152,9 +177,16 @@ def test_q8_prefill_zipf_512(orc, engine, skew):
     layer, moe = layer_for(engine, seed=1)
     h = synth.zipf_bias_tokens(layer, 3, 512, scale=skew)
     ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
-    got, t = moe.ffn_taps(h, dots=False)
+    got, t = moe.ffn_taps(h, dots=skew == 1.0)
     assert np.array_equal(t["ids"], ids)
     check_dispatch(t, ids, 512, layer.k)
+    if skew == 1.0:
+        # the matrix-core kernels' int32 block dots (exact gate/up word dots,
+        # int8 MFMA down) on a sample of the 4608 rows, hot expert included
+        hot = int(np.bincount(ids.ravel()).argmax())
+        p_hot = np.flatnonzero(t["pair_expert"] == hot)
+        check_block_dots_sampled(orc, layer, h, t, n_pairs=160, seed=5,
+                                 extra=(int(p_hot[0]), int(p_hot[-1]), 512 * 8, 512 * 8 + 511))
     check_output(ref, got, min_exact=0.0)  # int8 MFMA: f32 block sums in their own order
     again = moe.ffn(h)
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
@@ -335,10 +367,14 @@ def test_kquant_prefill(orc, engine, T):
     full_parity(orc, engine, layer, moe, h, block_dots=T == 64, min_exact=0.0)
 
 
-def _full_size(orc, moe, layer, h, exact_ids=True):
+def _full_size(orc, moe, layer, h, exact_ids=True, dots_sample=0):
     T = h.shape[0]
     ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
-    got, t = moe.ffn_taps(h, dots=False)
+    got, t = moe.ffn_taps(h, dots=dots_sample > 0)
+    if dots_sample:
+        check_block_dots_sampled(orc, layer, h, t, n_pairs=dots_sample, seed=9)
+        for key in ("gate_idots", "up_idots", "down_idots"):
+            t[key] = None
     if orc.detect_level() >= orc.AVX2:
         assert np.array_equal(t["logits"].view(np.uint32), logits.view(np.uint32)), "router logits differ"
     assert np.array_equal(t["ids"], ids), "top-k ids differ"
@@ -353,7 +389,49 @@ def test_kquant_full_size_2048(orc, engine):
     T = 2048 (the matrix-core kernels, exact Q4_K gate/up)."""
     print("case kquant full T=2048", flush=True)
     layer, moe = layer_for(engine, seed=33, types=(Q4K, Q4K, Q6K))
-    _full_size(orc, moe, layer, synth.make_tokens(2048, 2048))
+    # with the int32 block dots of a sample of the 18432 rows (exact Q4_K
+    # word dots, Q6_K half dots)
+    _full_size(orc, moe, layer, synth.make_tokens(2048, 2048), dots_sample=96)
+
+
+def test_kquant_full_size_decode(orc, engine):
+    """configs[3] at T = 1 and 5 with its full 256-expert router: the chain
+    kernels, bit-identical to the oracle."""
+    layer, moe = layer_for(engine, seed=33, types=(Q4K, Q4K, Q6K))
+    for T in (1, 5):
+        print(f"case kquant full T={T}", flush=True)
+        full_parity(orc, engine, layer, moe, synth.make_tokens(2100 + T, T, offsets=True))
+
+
+def test_bf16_stack_full_size(orc, engine):
+    """configs[4]'s step at its full size: x += moe(rms_norm(x)) through two
+    256-expert BF16 layers with a T = 4096 chunk (the pre-pass forms the
+    post_norm, the matrix-core router, the bf16 grouped GEMMs), against the
+    oracle after each layer (tolerance: the bf16 halves sum in their own
+    order)."""
+    print("case bf16 stack full T=4096", flush=True)
+    T, E, eps = 4096, 2048, 1e-6
+    layers = [synth.make_layer(seed=200 + l, types=(BF16, BF16, BF16)) for l in range(2)]
+    moes = [engine.moe(l) for l in layers]
+    rng = np.random.default_rng(8)
+    norms = [(1.0 + 0.02 * rng.standard_normal(E)).astype(np.float32) for _ in layers]
+    x = synth.make_tokens(701, T)
+    xd, nd = engine.malloc(x.nbytes), engine.malloc(E * 4)
+    try:
+        engine.h2d(xd, x)
+        prev = x.copy()
+        for layer, moe, w in zip(layers, moes, norms):
+            engine.h2d(nd, w)
+            moe.ffn_step_device(xd, nd, eps, T)
+            got = engine.d2h(np.empty_like(x), xd)
+            # the layer's own contribution, from the same input on both sides
+            # (x itself would hide its error in the RMS)
+            want = orc.moe(layer, orc.rms_norm(prev, w, eps), threads=8)
+            check_output(want, (got.astype(np.float64) - prev).astype(np.float32), min_exact=0.0)
+            prev = got
+    finally:
+        engine.free(xd)
+        engine.free(nd)
 
 
 def test_bf16_full_size_4096(orc, engine):
