@@ -65,9 +65,31 @@ def build(verbose=False, defines=(), out=OUT):
     return out
 
 
+PROBES = os.path.join(ROOT, "tests", "probes")
+
+
+def build_probes(verbose=False):
+    """The GPU test programs under tests/probes (each <name>.cpp, HIP, into
+    an executable <name> beside it)."""
+    outs = []
+    for src in sorted(f for f in os.listdir(PROBES) if f.endswith(".cpp")):
+        exe = os.path.join(PROBES, src[:-4])
+        cmd = [hipcc()] + FLAGS + ["-x", "hip", os.path.join(PROBES, src), "-o", exe]
+        if verbose:
+            print(" ".join(cmd))
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
+            raise RuntimeError(f"hipcc failed on {src}:\n{err}")
+        outs.append(exe)
+    return outs
+
+
 if __name__ == "__main__":
     # python -m biv_amd.build [-v] [-DNAME=VALUE ... -o PATH]: a variant build
     args = sys.argv[1:]
     defs = [a[2:] for a in args if a.startswith("-D")]
     out = args[args.index("-o") + 1] if "-o" in args else OUT
     print(build(verbose="-v" in args, defines=defs, out=out))
+    if not defs:
+        print(*build_probes(verbose="-v" in args), sep="\n")
