@@ -453,7 +453,7 @@ int scratch_fit(biv_hip_ctx *ctx, const biv_hip_moe *m, int T)
 // entry point calls no allocator.  Host code never passes `scratch` itself
 // (on the host it names a stand-in, not a device address): each context
 // resolves its GPU's copy with hipGetSymbolAddress at creation and uses that.
-constexpr size_t NOALLOC_BYTES = (size_t)32 << 20;
+constexpr size_t NOALLOC_BYTES = (size_t)48 << 20;
 static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
 
 // Carve the buffers of a forward of T tokens of layer m out of the context's

@@ -119,9 +119,9 @@ int biv_hip_moe_forward_device(biv_hip_ctx *ctx, const biv_hip_moe *moe, const f
 
 /* biv_hip_moe_forward_device for callers that cannot allocate (code under
  * HIP graph capture, tight serving loops): no counterpart in the reference.
- * It calls no allocator: its scratch is a fixed 32 MiB device buffer of the
+ * It calls no allocator: its scratch is a fixed 48 MiB device buffer of the
  * library, one per GPU, held until the process ends, which fits up to about
- * 240 tokens of a qwen35moe layer (n_embd 2048, n_ff 512, 256 experts, k 8);
+ * 350 tokens of a qwen35moe layer (n_embd 2048, n_ff 512, 256 experts, k 8);
  * larger n gives BIV_HIP_E_INVALID.  Every call on a GPU uses the same
  * buffer: calls that overlap on one GPU (two streams, two contexts) race. */
 int biv_hip_moe_forward_device_noalloc(biv_hip_ctx *ctx, const biv_hip_moe *moe, const float *h_dev, int n,

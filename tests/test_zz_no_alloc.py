@@ -17,7 +17,8 @@ def test_noalloc_matches_forward_device():
         layer = synth.make_layer(1)
         moe = eng.moe(layer)
         E = layer.n_embd
-        for T, add in ((40, False), (5, False), (1, True)):
+        # T = 256: the prefill pre-pass and the matrix-core router
+        for T, add in ((256, False), (40, False), (5, False), (1, True)):
             print(f"case noalloc T={T} add={add}", flush=True)
             h = synth.make_tokens(50 + T, T, offsets=True)
             x0 = synth.make_tokens(60 + T, T)
