@@ -579,6 +579,12 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     ra.norm_w = norm_w;
     ra.eps = eps;
     ra.hn = s.h_stage;
+    // BF16 gate/up on the matrix cores from the pre-pass's bf16 halves of h
+    const bool prep_split = mf_gu && T >= biv::prep_min_t();
+    if (prep_split) {
+        ra.xh = reinterpret_cast<uint4 *>(s.xh);
+        ra.xl = reinterpret_cast<uint4 *>(s.xl);
+    }
     if (norm_w) {
         if (h == s.h_stage) return fail(ctx, BIV_HIP_E_INVALID, "post_norm input aliases its output");
         h = s.h_stage; // every later use of h takes the normalised rows
@@ -623,7 +629,7 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
             g.u_max = u_max;
             g.chunk = chunk;
             g.sh_chunk = biv::MFMA_TOK_TILE;
-            HIP_TRY(ctx, biv::launch_split_bf16(h, T, E, s.xh, s.xl, st), "split h");
+            if (!prep_split) HIP_TRY(ctx, biv::launch_split_bf16(h, T, E, s.xh, s.xl, st), "split h");
             HIP_TRY(ctx, biv::launch_mfma_gateup(g, st), "expert gate/up (mfma)");
         } else if (mq_gu) {
             a.sh_chunk = biv::MFMA_Q8_TILE;

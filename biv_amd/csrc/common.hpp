@@ -80,7 +80,22 @@ struct RouterArgs {
     const float *norm_w;
     float eps;
     float *hn;
+    // With xh (BF16 experts at T >= prep_min_t()): the bf16 hi / lo halves of
+    // the (normalised) rows in the matrix-core chunk order, as
+    // launch_split_bf16 writes them, formed by the pre-pass
+    uint4 *xh, *xl;
 };
+// tokens from which launch_router runs the prefill pre-pass (and the
+// matrix-core router)
+int prep_min_t();
+
+// bf16 bits of x, round to nearest, ties to even (finite x); NaN stays NaN
+__device__ inline uint32_t bf16_bits(float x)
+{
+    const uint32_t u = __float_as_uint(x);
+    if (x != x) return 0x7FC0u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
 // router logits + gate_inp logit + Q8 quantisation of h
 hipError_t launch_router(const RouterArgs &a, hipStream_t st);
 // route every token, then sort the pairs into dispatch order (`work`:

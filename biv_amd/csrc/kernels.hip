@@ -697,7 +697,9 @@ __device__ inline void wave_lds_sync()
 //     (quant.rs:1177-1207), chain L in lane L, then the tree;
 //   the Q8 for the experts of the (normalised) row: it goes through LDS
 //     (32-element blocks at a 36-float pitch) so that lane b quantises
-//     block b.
+//     block b;
+//   with xh, the bf16 hi / lo halves of the row for BF16 experts (from the
+//     LDS copy, as k_split_bf16 forms them).
 // Lanes 32-63 repeat the chains of lanes 0-31 (the shuffle tree stays within
 // each half); each half writes half of the row (to hn and LDS).  The norm
 // weights and the gate row, the chains' operands, are staged in LDS once per
@@ -763,6 +765,25 @@ template <int NS> __global__ __launch_bounds__(64 * PREP_TOK) void k_prep(Router
         quant_block_lds(reinterpret_cast<const float4 *>(r + lane * PREP_PITCH), E, lane,
                         reinterpret_cast<int *>(a.xq + (size_t)t * E), a.xd + (size_t)t * (E / 32),
                         a.xs + (size_t)t * (E / 32));
+    if (a.xh) {
+        // the bf16 halves for the matrix-core gate/up: 16-byte chunk 16 g + c
+        // of the row holds elements 128 g + 16 m + c, m = 0..7
+        for (int ch = lane; ch < E / 8; ch += 64) {
+            const int g = ch >> 4, c = ch & 15;
+            uint32_t hb[8], lb[8];
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                const int e = 128 * g + 16 * m + c;
+                const float x = r[(e >> 5) * PREP_PITCH + (e & 31)];
+                hb[m] = bf16_bits(x);
+                lb[m] = bf16_bits(x - __uint_as_float(hb[m] << 16));
+            }
+            a.xh[(size_t)t * (E / 8) + ch] = make_uint4(hb[0] | hb[1] << 16, hb[2] | hb[3] << 16, hb[4] | hb[5] << 16,
+                                                        hb[6] | hb[7] << 16);
+            a.xl[(size_t)t * (E / 8) + ch] = make_uint4(lb[0] | lb[1] << 16, lb[2] | lb[3] << 16, lb[4] | lb[5] << 16,
+                                                        lb[6] | lb[7] << 16);
+        }
+    }
 }
 
 
@@ -2315,6 +2336,8 @@ hipError_t launch_rms_norm(const float *x, float *y, const float *w, int rows, i
 #ifndef BIV_ROUTER_T1_NTH
 #define BIV_ROUTER_T1_NTH 64
 #endif
+int prep_min_t() { return RT_MIN_T; }
+
 hipError_t launch_router(const RouterArgs &a0, hipStream_t st)
 {
     RouterArgs a = a0;

@@ -57,13 +57,6 @@ template <int RUN> inline unsigned slot_grid(int slots, int n_rt)
     return (unsigned)(N_XCD * ((runs + N_XCD - 1) / N_XCD) * RUN * n_rt);
 }
 
-__device__ inline uint32_t bf16_bits(float x)
-{
-    // round to nearest, ties to even (finite x); NaN stays NaN
-    const uint32_t u = __float_as_uint(x);
-    if (x != x) return 0x7FC0u;
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
 
 __device__ inline bf16x8 as_bf16x8(const uint4 &v) { return __builtin_bit_cast(bf16x8, v); }
 
