@@ -82,7 +82,9 @@ int biv_hip_sync(biv_hip_ctx *ctx);
 
 /* Upload one matrix of `rows` rows of `cols` elements in ggml layout
  * (Weight::new, engine/src/ops.rs:22-33): `data` holds rows * row_size(cols)
- * bytes on the host.  Used for the router, the shared expert and its gate. */
+ * bytes on the host.  Used for the router, the shared expert and its gate.
+ * An F32 matrix takes twice its bytes on the device: the rows in the chain
+ * layout of the decode router and as given, for the prefill router. */
 int biv_hip_upload_weight(biv_hip_ctx *ctx, int ggml_type, size_t cols, size_t rows, const void *data,
                           biv_hip_weight **out);
 
