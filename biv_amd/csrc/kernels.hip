@@ -1221,14 +1221,80 @@ __global__ __launch_bounds__(MAX_EXPERTS *DS_SPLIT) void k_dispatch_scan(int n_e
     for (int u = n_used + e; u < dp.slot_cap; u += MAX_EXPERTS) reinterpret_cast<int4 *>(&dp.slots[u])[0] = make_int4(0, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(256) void k_dispatch_place(int n_expert, int k, int T, int nb, int chunk, Dispatch dp,
-                                                        const int *work)
+// Up to DP_FUSE_NB blocks, k_dispatch_place<true> runs k_dispatch_scan's
+// arithmetic itself (one launch fewer): every workgroup reads the whole
+// count table (a column of at most DP_FUSE_NB counts per thread, all loads
+// in flight at once) for its block's first ranks and the experts' first
+// positions and slots; workgroup 0 writes the slot records.  The same
+// integer sums, so the same dispatch.
+constexpr int DP_FUSE_NB = 32;
+
+template <bool FUSED>
+__global__ __launch_bounds__(MAX_EXPERTS) void k_dispatch_place(int n_expert, int k, int T, int nb, int chunk,
+                                                                Dispatch dp, const int *work)
 {
     __shared__ unsigned mask[MAX_EXPERTS];
+    __shared__ int base_s[FUSED ? MAX_EXPERTS : 1], first_s[FUSED ? MAX_EXPERTS : 1],
+        sfirst_s[FUSED ? MAX_EXPERTS : 1];
     const int b = blockIdx.x, t0 = b * RB_TOKS, nt = min(RB_TOKS, T - t0);
+    const int *base, *first, *sfirst;
+    if constexpr (FUSED) {
+        const int e = threadIdx.x, lane = e & (WAVE - 1), w = e >> 6;
+        int v[DP_FUSE_NB];
+#pragma unroll
+        for (int j = 0; j < DP_FUSE_NB; j++) v[j] = j < nb ? work[(size_t)j * MAX_EXPERTS + e] : 0;
+        int tot = 0, bse = 0;
+#pragma unroll
+        for (int j = 0; j < DP_FUSE_NB; j++) {
+            if (j == b) bse = tot;
+            tot += v[j];
+        }
+        if (e >= n_expert) tot = 0;
+        const int nsl = (tot + chunk - 1) / chunk;
+        // exclusive scans over the experts of the pair and slot totals
+        __shared__ int wsum[2][MAX_EXPERTS / WAVE];
+        int x = tot, y = nsl;
+#pragma unroll
+        for (int off = 1; off < WAVE; off <<= 1) {
+            const int xs = __shfl_up(x, off), ys = __shfl_up(y, off);
+            if (lane >= off) {
+                x += xs;
+                y += ys;
+            }
+        }
+        if (lane == WAVE - 1) {
+            wsum[0][w] = x;
+            wsum[1][w] = y;
+        }
+        __syncthreads();
+        int px = 0, py = 0, n_used = 0;
+        for (int i = 0; i < MAX_EXPERTS / WAVE; i++) {
+            if (i < w) {
+                px += wsum[0][i];
+                py += wsum[1][i];
+            }
+            n_used += wsum[1][i];
+        }
+        const int fst = px + x - tot, sfst = py + y - nsl;
+        base_s[e] = bse;
+        first_s[e] = fst;
+        sfirst_s[e] = sfst;
+        if (b == 0) {
+            for (int j = 0; j < nsl; j++)
+                reinterpret_cast<int4 *>(&dp.slots[sfst + j])[0] =
+                    make_int4(e, fst + j * chunk, min(chunk, tot - j * chunk), n_used);
+            for (int u = n_used + e; u < dp.slot_cap; u += MAX_EXPERTS)
+                reinterpret_cast<int4 *>(&dp.slots[u])[0] = make_int4(0, 0, 0, 0);
+        }
+        base = base_s;
+        first = first_s;
+        sfirst = sfirst_s;
+    } else {
+        base = work + (size_t)b * MAX_EXPERTS;
+        first = work + (size_t)nb * MAX_EXPERTS;
+        sfirst = work + (size_t)(nb + 1) * MAX_EXPERTS;
+    }
     block_masks(dp.ids, n_expert, k, T, b, mask);
-    const int *base = work + (size_t)b * MAX_EXPERTS, *first = work + (size_t)nb * MAX_EXPERTS,
-              *sfirst = work + (size_t)(nb + 1) * MAX_EXPERTS;
     for (int i = threadIdx.x; i < nt * k; i += blockDim.x) {
         const int tl = i / k, t = t0 + tl;
         const int e = dp.ids[(size_t)t0 * k + i];
@@ -2404,9 +2470,11 @@ hipError_t launch_route_sort(const float *logits, int n_expert, int k, int T, in
     const int groups = T <= RS_WAVES ? 1 : (T + RS_WAVES - 1) / RS_WAVES;
     const int threads = groups == 1 ? WAVE * T : RS_THREADS; // a wavefront per token
     k_route_sort<<<groups, threads, 0, st>>>(logits, n_expert, k, T, chunk, dp, work);
-    if (groups > 1) {
+    if (groups > 1 && groups <= DP_FUSE_NB) {
+        k_dispatch_place<true><<<groups, MAX_EXPERTS, 0, st>>>(n_expert, k, T, groups, chunk, dp, work);
+    } else if (groups > 1) {
         k_dispatch_scan<<<1, MAX_EXPERTS * DS_SPLIT, 0, st>>>(n_expert, groups, chunk, dp, work);
-        k_dispatch_place<<<groups, 256, 0, st>>>(n_expert, k, T, groups, chunk, dp, work);
+        k_dispatch_place<false><<<groups, MAX_EXPERTS, 0, st>>>(n_expert, k, T, groups, chunk, dp, work);
     }
     return hipGetLastError();
 }
