@@ -1152,41 +1152,85 @@ __device__ void route_block_counts(const int *ids, int n_expert, int k, int T, i
 }
 
 constexpr int DS_SPLIT = 4; // threads per expert column in k_dispatch_scan
+// Up to DS_RUNS * 16 blocks (T <= 4096) a thread of k_dispatch_scan takes
+// four adjacent experts (one 16-byte load per block) over a run of at most
+// 16 blocks, all its loads in flight at once.
+constexpr int DS_RUNS = MAX_EXPERTS * DS_SPLIT / (MAX_EXPERTS / 4);
 __global__ __launch_bounds__(MAX_EXPERTS *DS_SPLIT) void k_dispatch_scan(int n_expert, int nb, int chunk, Dispatch dp,
                                                                          int *work)
 {
-    // DS_SPLIT threads per expert, each over a run of the blocks: its sum,
-    // the runs' offsets, then its blocks' exclusive prefixes (16 loads in
-    // flight at a time; integer sums, so the result does not depend on the
-    // split)
+    // Each block's exclusive prefix per expert, in place, and each expert's
+    // total (integer sums: the result does not depend on how the blocks are
+    // split between threads)
     const int e = threadIdx.x & (MAX_EXPERTS - 1), qs = threadIdx.x / MAX_EXPERTS;
     const int lane = e & (WAVE - 1), w = e >> 6;
-    const int nbq = (nb + DS_SPLIT - 1) / DS_SPLIT, b_lo = min(nb, qs * nbq), b_hi = min(nb, b_lo + nbq);
-    __shared__ int part[DS_SPLIT][MAX_EXPERTS];
-    int sum = 0;
-    for (int b0 = b_lo; b0 < b_hi; b0 += 16) {
-        int v[16];
-#pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = b0 + j < b_hi ? work[(size_t)(b0 + j) * MAX_EXPERTS + e] : 0;
-#pragma unroll
-        for (int j = 0; j < 16; j++) sum += v[j];
-    }
-    part[qs][e] = sum;
-    __syncthreads();
     int run = 0;
-    for (int i = 0; i < qs; i++) run += part[i][e];
-    for (int b0 = b_lo; b0 < b_hi; b0 += 16) {
-        int v[16];
+    if (nb <= DS_RUNS * 16) {
+        __shared__ int part[DS_RUNS][MAX_EXPERTS];
+        const int q4 = threadIdx.x % (MAX_EXPERTS / 4), r = threadIdx.x / (MAX_EXPERTS / 4);
+        const int nbr = (nb + DS_RUNS - 1) / DS_RUNS, lo = min(nb, r * nbr), hi = min(nb, lo + nbr);
+        int4 *w4 = reinterpret_cast<int4 *>(work);
+        int4 v[16];
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = b0 + j < b_hi ? work[(size_t)(b0 + j) * MAX_EXPERTS + e] : 0;
+        for (int j = 0; j < 16; j++)
+            v[j] = lo + j < hi ? w4[(size_t)(lo + j) * (MAX_EXPERTS / 4) + q4] : make_int4(0, 0, 0, 0);
+        int4 sm = make_int4(0, 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            if (b0 + j < b_hi) work[(size_t)(b0 + j) * MAX_EXPERTS + e] = run;
-            run += v[j];
+            sm.x += v[j].x;
+            sm.y += v[j].y;
+            sm.z += v[j].z;
+            sm.w += v[j].w;
         }
+        reinterpret_cast<int4 *>(&part[r][0])[q4] = sm;
+        __syncthreads();
+        int4 rn = make_int4(0, 0, 0, 0);
+        for (int i = 0; i < r; i++) {
+            const int4 pv = reinterpret_cast<const int4 *>(&part[i][0])[q4];
+            rn.x += pv.x;
+            rn.y += pv.y;
+            rn.z += pv.z;
+            rn.w += pv.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            if (lo + j < hi) w4[(size_t)(lo + j) * (MAX_EXPERTS / 4) + q4] = rn;
+            rn.x += v[j].x;
+            rn.y += v[j].y;
+            rn.z += v[j].z;
+            rn.w += v[j].w;
+        }
+        for (int i = 0; i < DS_RUNS; i++) run += part[i][e];
+    } else {
+        // DS_SPLIT threads per expert, each over a run of the blocks: its
+        // sum, the runs' offsets, then its blocks' prefixes (16 loads in
+        // flight at a time, twice)
+        __shared__ int part[DS_SPLIT][MAX_EXPERTS];
+        const int nbq = (nb + DS_SPLIT - 1) / DS_SPLIT, b_lo = min(nb, qs * nbq), b_hi = min(nb, b_lo + nbq);
+        int sum = 0;
+        for (int b0 = b_lo; b0 < b_hi; b0 += 16) {
+            int v[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = b0 + j < b_hi ? work[(size_t)(b0 + j) * MAX_EXPERTS + e] : 0;
+#pragma unroll
+            for (int j = 0; j < 16; j++) sum += v[j];
+        }
+        part[qs][e] = sum;
+        __syncthreads();
+        for (int i = 0; i < qs; i++) run += part[i][e];
+        for (int b0 = b_lo; b0 < b_hi; b0 += 16) {
+            int v[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = b0 + j < b_hi ? work[(size_t)(b0 + j) * MAX_EXPERTS + e] : 0;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                if (b0 + j < b_hi) work[(size_t)(b0 + j) * MAX_EXPERTS + e] = run;
+                run += v[j];
+            }
+        }
+        run = 0;
+        for (int i = 0; i < DS_SPLIT; i++) run += part[i][e];
     }
-    run = 0;
-    for (int i = 0; i < DS_SPLIT; i++) run += part[i][e];
     const int tot = e < n_expert ? run : 0, nsl = (tot + chunk - 1) / chunk;
     // exclusive scans over the experts of the pair and slot totals
     __shared__ int wsum[2][MAX_EXPERTS / WAVE];

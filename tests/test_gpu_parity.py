@@ -152,10 +152,21 @@ def test_q8_small_layer(orc, engine, T):
     print(f"case q8 small T={T}", flush=True)
     layer, moe = layer_for(engine, seed=21, n_expert=32)
     h = synth.make_tokens(100 + T, T, offsets=True)
-    # T = 1100: 69 blocks of 16 tokens, so a dispatch-scan thread sums a run
-    # of 18 blocks ending in a partial group of 16
+    # T = 1100: 69 blocks of 16 tokens, so the dispatch scan's runs are 5
+    # blocks long and the last one is partial
     full_parity(orc, engine, layer, moe, h, block_dots=T <= 9 or T in (64, 65),
                 min_exact=0.9999 if T < 64 else 0.0)
+
+
+@pytest.mark.parametrize("T", [4096, 4200])
+def test_dispatch_large_T(orc, engine, T):
+    """The counting sort at the block counts of long prefills: 256 blocks of
+    16 tokens (every scan run full, counts held in registers) and 263 (past
+    them: two passes over the counts).  A small layer keeps the oracle quick."""
+    print(f"case dispatch T={T}", flush=True)
+    layer, moe = layer_for(engine, seed=23, n_embd=512, n_expert=32)
+    h = synth.make_tokens(300 + T, T, n_embd=512, offsets=True)
+    full_parity(orc, engine, layer, moe, h, block_dots=False, min_exact=0.0)
 
 
 @pytest.mark.parametrize("T", [1, 5, 40])
