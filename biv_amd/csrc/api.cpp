@@ -624,6 +624,13 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
             g.xl = reinterpret_cast<const uint4 *>(s.xl);
             g.dp = s.dp;
             g.out = s.act;
+            if (mf_dn) {
+                // the intermediate goes out as the bf16 halves the down
+                // kernel reads, in the f32 intermediate's bytes (no split launch)
+                g.out = nullptr;
+                g.xo_h = reinterpret_cast<uint4 *>(s.act);
+                g.xo_l = g.xo_h + (size_t)(has_shared ? P + T : P) * ff / 8;
+            }
             g.T = T;
             g.P = P;
             g.u_max = u_max;
@@ -700,8 +707,14 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
             biv::MfArgs g{};
             g.a = d.a;
             g.sa = d.sa;
-            g.xh = reinterpret_cast<const uint4 *>(s.xh);
-            g.xl = reinterpret_cast<const uint4 *>(s.xl);
+            if (mf_gu) {
+                // gate/up wrote the halves (in the intermediate's bytes)
+                g.xh = reinterpret_cast<const uint4 *>(s.act);
+                g.xl = g.xh + (size_t)(has_shared ? P + T : P) * ff / 8;
+            } else {
+                g.xh = reinterpret_cast<const uint4 *>(s.xh);
+                g.xl = reinterpret_cast<const uint4 *>(s.xl);
+            }
             g.dp = s.dp;
             g.out = s.y;
             g.T = T;
@@ -709,7 +722,8 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
             g.u_max = u_max;
             g.chunk = chunk;
             g.sh_chunk = biv::MFMA_TOK_TILE;
-            HIP_TRY(ctx, biv::launch_split_bf16(s.act, has_shared ? P + T : P, ff, s.xh, s.xl, st), "split act");
+            if (!mf_gu)
+                HIP_TRY(ctx, biv::launch_split_bf16(s.act, has_shared ? P + T : P, ff, s.xh, s.xl, st), "split act");
             HIP_TRY(ctx, biv::launch_mfma_down(g, st), "expert down (mfma)");
         } else if (mq_dn) {
             d.sh_chunk = biv::MFMA_Q8_TILE;

@@ -182,6 +182,7 @@ struct MfArgs {
     const uint4 *xl;   // lo halves
     Dispatch dp;
     float *out;        // [P + T][rows]
+    uint4 *xo_h, *xo_l; // gate/up: instead of out, the outputs' bf16 halves (as k_split_bf16 writes them)
     int T, P;
     int n_rt;          // row tiles (set by the launcher)
     int u_max;         // grid slots of the routed experts

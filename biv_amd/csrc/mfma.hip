@@ -131,6 +131,8 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     constexpr int BR = ROW_TILE * NB;  // weight rows of a tile
     constexpr int A_SLOTS = 2 * SK * TOK_TILE, B_SLOTS = SK * BR;
     static_assert(A_SLOTS % NTH == 0 && B_SLOTS % NTH == 0, "tile shapes");
+    // separate arrays: the compiler then tells the buffers a DMA writes apart
+    // (one array would make it wait for every DMA before each LDS read)
     __shared__ uint4 sA0[A_SLOTS], sA1[A_SLOTS], sA2[A_SLOTS], sB0[B_SLOTS], sB1[B_SLOTS], sB2[B_SLOTS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 31, kg = lane >> 5;
@@ -260,15 +262,60 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     }
     if (s < NS) step(s, sA0, sB0, sA2, sB2);
     if (s + 1 < NS) step(s + 1, sA1, sB1, sA0, sB0);
-    // the exp table in LDS for the SwiGLU (the tiles are no longer read)
-    uint64_t *tab = reinterpret_cast<uint64_t *>(sA0);
+    // the exp table in LDS for the SwiGLU
+    __shared__ uint64_t tab[GATEUP ? 32 : 1];
     if (GATEUP) {
-        __syncthreads();
         if (tid < 32) tab[tid] = exp_tab[tid];
-        __syncthreads();
+        __syncthreads(); // (also: every wave is done with the ring)
     }
     // D of a 32 x 32 block: lane (li, kg), register j: row (pair) (j / 4) * 8
     // + 4 kg + j % 4, column (weight row) li
+    if constexpr (GATEUP) if (a.xo_h) {
+        // the intermediate's bf16 hi / lo halves in the chunk order, as
+        // k_split_bf16 forms them: the tile's SwiGLU values [pair][row]
+        // through LDS (the ring's buffers, PA pairs' rows in each A buffer
+        // and PB in each B buffer, EP floats apart), then 16-byte chunks:
+        // this row tile is elements 128 rt .. 128 rt + 127 of each row, so
+        // chunk 16 rt + L holds its rows 16 m + L
+        constexpr int EP = 136, PA = A_SLOTS * 4 / EP, PB = B_SLOTS * 4 / EP;
+        static_assert(ROW_TILE == 128, "one 128-element span per row tile");
+        static_assert(3 * (PA + PB) >= TOK_TILE, "the tile fits in the ring");
+        auto trow = [&](int p) -> float * {
+            if (p < 3 * PA) {
+                const int i = p / PA;
+                return reinterpret_cast<float *>(i == 0 ? sA0 : i == 1 ? sA1 : sA2) + (p - PA * i) * EP;
+            }
+            const int i = (p - 3 * PA) / PB;
+            return reinterpret_cast<float *>(i == 0 ? sB0 : i == 1 ? sB1 : sB2) + (p - 3 * PA - PB * i) * EP;
+        };
+#pragma unroll
+        for (int tb = 0; tb < 2; tb++)
+            if (tb ? live1 : live0)
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+                    for (int j = 0; j < 16; j++) {
+                        const int ti = wt * 64 + tb * 32 + (j / 4) * 8 + 4 * kg + (j % 4);
+                        trow(ti)[wr * 32 * RB + rb * 32 + li] =
+                            silu_mul_t(acc[tb][rb][0][j], acc[tb][rb][NB - 1][j], tab);
+                    }
+        __syncthreads();
+        const int nc = rows / 8;
+        for (int x = tid; x < cnt * 16; x += NTH) {
+            const int p = x >> 4, L = x & 15;
+            uint32_t h[8], lo[8];
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                const float v = trow(p)[16 * m + L];
+                h[m] = bf16_bits(v);
+                lo[m] = bf16_bits(v - __uint_as_float(h[m] << 16));
+            }
+            const size_t c = (size_t)(beg + p) * nc + 16 * rt + L;
+            a.xo_h[c] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
+            a.xo_l[c] = make_uint4(lo[0] | lo[1] << 16, lo[2] | lo[3] << 16, lo[4] | lo[5] << 16, lo[6] | lo[7] << 16);
+        }
+        return;
+    }
 #pragma unroll
     for (int tb = 0; tb < 2; tb++)
 #pragma unroll
