@@ -227,8 +227,10 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
                     for (int rb = 0; rb < RB; rb++)
 #pragma unroll
                         for (int q = 0; q < NB; q++)
-                            acc[tb][rb][q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                                as_bf16x8(xa[tb][hl]), as_bf16x8(wb[rb][q]), acc[tb][rb][q], 0, 0, 0);
+                            acc[tb][rb][q] = GATEUP ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                                          as_bf16x8(wb[rb][q]), as_bf16x8(xa[tb][hl]), acc[tb][rb][q], 0, 0, 0)
+                                                    : __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                                          as_bf16x8(xa[tb][hl]), as_bf16x8(wb[rb][q]), acc[tb][rb][q], 0, 0, 0);
         }
     };
     // three buffers, loads two stages ahead: stage s is in buffer s % 3
@@ -268,8 +270,13 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         if (tid < 32) tab[tid] = exp_tab[tid];
         __syncthreads(); // (also: every wave is done with the ring)
     }
-    // D of a 32 x 32 block: lane (li, kg), register j: row (pair) (j / 4) * 8
-    // + 4 kg + j % 4, column (weight row) li
+    // D of a 32 x 32 block.  gate/up (weights as A, the pairs as B): lane
+    // (li, kg), registers 4 q .. 4 q + 3: weight rows 8 q + 4 kg .. 8 q + 4 kg
+    // + 3 of the block, pair li: four consecutive outputs, one 16-byte store.
+    // down (the pairs as A): register j is pair 8 (j / 4) + 4 kg + j % 4,
+    // weight row li: a half wave stores 32 consecutive outputs (down's large
+    // output keeps whole 128-byte segments that way; 16-byte stores across 32
+    // rows measured slower)
     if constexpr (GATEUP) if (a.xo_h) {
         // the intermediate's bf16 hi / lo halves in the chunk order, as
         // k_split_bf16 forms them: the tile's SwiGLU values [pair][row]
@@ -294,10 +301,14 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
                 for (int rb = 0; rb < RB; rb++)
 #pragma unroll
-                    for (int j = 0; j < 16; j++) {
-                        const int ti = wt * 64 + tb * 32 + (j / 4) * 8 + 4 * kg + (j % 4);
-                        trow(ti)[wr * 32 * RB + rb * 32 + li] =
-                            silu_mul_t(acc[tb][rb][0][j], acc[tb][rb][NB - 1][j], tab);
+                    for (int q = 0; q < 4; q++) {
+                        float4 v;
+                        v.x = silu_mul_t(acc[tb][rb][0][4 * q], acc[tb][rb][NB - 1][4 * q], tab);
+                        v.y = silu_mul_t(acc[tb][rb][0][4 * q + 1], acc[tb][rb][NB - 1][4 * q + 1], tab);
+                        v.z = silu_mul_t(acc[tb][rb][0][4 * q + 2], acc[tb][rb][NB - 1][4 * q + 2], tab);
+                        v.w = silu_mul_t(acc[tb][rb][0][4 * q + 3], acc[tb][rb][NB - 1][4 * q + 3], tab);
+                        *reinterpret_cast<float4 *>(trow(wt * 64 + tb * 32 + li) + wr * 32 * RB + rb * 32 + 8 * q +
+                                                    4 * kg) = v;
                     }
         __syncthreads();
         const int nc = rows / 8;
@@ -316,20 +327,36 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         }
         return;
     }
+    if constexpr (GATEUP) {
 #pragma unroll
-    for (int tb = 0; tb < 2; tb++)
+        for (int tb = 0; tb < 2; tb++) {
+            const int ti = wt * 64 + tb * 32 + li;
+            if (ti < cnt)
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++)
+                for (int rb = 0; rb < RB; rb++)
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const int ti = wt * 64 + tb * 32 + (j / 4) * 8 + 4 * kg + (j % 4);
-                const int row = r0 + wr * 32 * RB + rb * 32 + li;
-                if (ti < cnt) {
-                    const float v = GATEUP ? silu_mul_t(acc[tb][rb][0][j], acc[tb][rb][NB - 1][j], tab)
-                                           : acc[tb][rb][0][j];
-                    a.out[(size_t)(beg + ti) * rows + row] = v;
+                    for (int q = 0; q < 4; q++) {
+                        const int row = r0 + wr * 32 * RB + rb * 32 + 8 * q + 4 * kg;
+                        float4 v;
+                        v.x = silu_mul_t(acc[tb][rb][0][4 * q], acc[tb][rb][NB - 1][4 * q], tab);
+                        v.y = silu_mul_t(acc[tb][rb][0][4 * q + 1], acc[tb][rb][NB - 1][4 * q + 1], tab);
+                        v.z = silu_mul_t(acc[tb][rb][0][4 * q + 2], acc[tb][rb][NB - 1][4 * q + 2], tab);
+                        v.w = silu_mul_t(acc[tb][rb][0][4 * q + 3], acc[tb][rb][NB - 1][4 * q + 3], tab);
+                        *reinterpret_cast<float4 *>(a.out + (size_t)(beg + ti) * rows + row) = v;
+                    }
+        }
+    } else {
+#pragma unroll
+        for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const int ti = wt * 64 + tb * 32 + (j / 4) * 8 + 4 * kg + (j % 4);
+                    const int row = r0 + wr * 32 * RB + rb * 32 + li;
+                    if (ti < cnt) a.out[(size_t)(beg + ti) * rows + row] = acc[tb][rb][0][j];
                 }
-            }
+    }
 }
 
 
