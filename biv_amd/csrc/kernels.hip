@@ -1151,6 +1151,50 @@ __device__ void route_block_counts(const int *ids, int n_expert, int k, int T, i
     for (int e = threadIdx.x; e < MAX_EXPERTS; e += blockDim.x) work[(size_t)b * MAX_EXPERTS + e] = __popc(mask[e]);
 }
 
+// The experts' exclusive scans, one thread per expert e (lane, wave w of
+// MAX_EXPERTS / WAVE; every thread of the workgroup calls it, `writer` those
+// of the first MAX_EXPERTS): its first dispatch position (pairs in expert
+// order) and its first slot.  Slots are numbered with the experts whose
+// pairs fill at most half a slot last: their cheap units then go out last
+// and fill the grid's tail.  An expert's slots stay consecutive (their
+// workgroups share its weights through L2).  n_used: the slots in use.
+__device__ inline void expert_scan(int tot, int chunk, bool writer, int (&wsum)[3][MAX_EXPERTS / WAVE], int &first,
+                                   int &sfirst, int &n_used)
+{
+    const int lane = threadIdx.x & (WAVE - 1), w = (threadIdx.x & (MAX_EXPERTS - 1)) >> 6;
+    const int nsl = (tot + chunk - 1) / chunk;
+    const bool light = tot > 0 && 2 * tot <= chunk;
+    int x = tot, yh = light ? 0 : nsl, yl = light ? nsl : 0;
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+        const int xs = __shfl_up(x, off), hs = __shfl_up(yh, off), ls = __shfl_up(yl, off);
+        if (lane >= off) {
+            x += xs;
+            yh += hs;
+            yl += ls;
+        }
+    }
+    if (writer && lane == WAVE - 1) {
+        wsum[0][w] = x;
+        wsum[1][w] = yh;
+        wsum[2][w] = yl;
+    }
+    __syncthreads();
+    int px = 0, ph = 0, pl = 0, n_heavy = 0, n_light = 0;
+    for (int i = 0; i < MAX_EXPERTS / WAVE; i++) {
+        if (i < w) {
+            px += wsum[0][i];
+            ph += wsum[1][i];
+            pl += wsum[2][i];
+        }
+        n_heavy += wsum[1][i];
+        n_light += wsum[2][i];
+    }
+    first = px + x - tot;
+    sfirst = light ? n_heavy + pl + yl - nsl : ph + yh - nsl;
+    n_used = n_heavy + n_light;
+}
+
 constexpr int DS_SPLIT = 4; // threads per expert column in k_dispatch_scan
 // Up to DS_RUNS * 16 blocks (T <= 4096) a thread of k_dispatch_scan takes
 // four adjacent experts (one 16-byte load per block) over a run of at most
@@ -1163,7 +1207,6 @@ __global__ __launch_bounds__(MAX_EXPERTS *DS_SPLIT) void k_dispatch_scan(int n_e
     // total (integer sums: the result does not depend on how the blocks are
     // split between threads)
     const int e = threadIdx.x & (MAX_EXPERTS - 1), qs = threadIdx.x / MAX_EXPERTS;
-    const int lane = e & (WAVE - 1), w = e >> 6;
     int run = 0;
     if (nb <= DS_RUNS * 16) {
         __shared__ int part[DS_RUNS][MAX_EXPERTS];
@@ -1232,31 +1275,10 @@ __global__ __launch_bounds__(MAX_EXPERTS *DS_SPLIT) void k_dispatch_scan(int n_e
         for (int i = 0; i < DS_SPLIT; i++) run += part[i][e];
     }
     const int tot = e < n_expert ? run : 0, nsl = (tot + chunk - 1) / chunk;
-    // exclusive scans over the experts of the pair and slot totals
-    __shared__ int wsum[2][MAX_EXPERTS / WAVE];
-    int x = tot, y = nsl;
-#pragma unroll
-    for (int off = 1; off < WAVE; off <<= 1) {
-        const int xs = __shfl_up(x, off), ys = __shfl_up(y, off);
-        if (lane >= off) {
-            x += xs;
-            y += ys;
-        }
-    }
-    if (lane == WAVE - 1 && qs == 0) {
-        wsum[0][w] = x;
-        wsum[1][w] = y;
-    }
-    __syncthreads();
-    if (qs != 0) return; // the experts' scans and records: one thread per expert
-    int px = 0, py = 0;
-    for (int i = 0; i < w; i++) {
-        px += wsum[0][i];
-        py += wsum[1][i];
-    }
-    const int first = px + x - tot, sfirst = py + y - nsl;
-    int n_used = 0;
-    for (int i = 0; i < MAX_EXPERTS / WAVE; i++) n_used += wsum[1][i];
+    __shared__ int wsum[3][MAX_EXPERTS / WAVE];
+    int first, sfirst, n_used;
+    expert_scan(tot, chunk, qs == 0, wsum, first, sfirst, n_used);
+    if (qs != 0) return; // the records: one thread per expert
     work[(size_t)nb * MAX_EXPERTS + e] = first;
     work[(size_t)(nb + 1) * MAX_EXPERTS + e] = sfirst;
     for (int j = 0; j < nsl; j++)
@@ -1283,7 +1305,7 @@ __global__ __launch_bounds__(MAX_EXPERTS) void k_dispatch_place(int n_expert, in
     const int b = blockIdx.x, t0 = b * RB_TOKS, nt = min(RB_TOKS, T - t0);
     const int *base, *first, *sfirst;
     if constexpr (FUSED) {
-        const int e = threadIdx.x, lane = e & (WAVE - 1), w = e >> 6;
+        const int e = threadIdx.x;
         int v[DP_FUSE_NB];
 #pragma unroll
         for (int j = 0; j < DP_FUSE_NB; j++) v[j] = j < nb ? work[(size_t)j * MAX_EXPERTS + e] : 0;
@@ -1295,31 +1317,9 @@ __global__ __launch_bounds__(MAX_EXPERTS) void k_dispatch_place(int n_expert, in
         }
         if (e >= n_expert) tot = 0;
         const int nsl = (tot + chunk - 1) / chunk;
-        // exclusive scans over the experts of the pair and slot totals
-        __shared__ int wsum[2][MAX_EXPERTS / WAVE];
-        int x = tot, y = nsl;
-#pragma unroll
-        for (int off = 1; off < WAVE; off <<= 1) {
-            const int xs = __shfl_up(x, off), ys = __shfl_up(y, off);
-            if (lane >= off) {
-                x += xs;
-                y += ys;
-            }
-        }
-        if (lane == WAVE - 1) {
-            wsum[0][w] = x;
-            wsum[1][w] = y;
-        }
-        __syncthreads();
-        int px = 0, py = 0, n_used = 0;
-        for (int i = 0; i < MAX_EXPERTS / WAVE; i++) {
-            if (i < w) {
-                px += wsum[0][i];
-                py += wsum[1][i];
-            }
-            n_used += wsum[1][i];
-        }
-        const int fst = px + x - tot, sfst = py + y - nsl;
+        __shared__ int wsum[3][MAX_EXPERTS / WAVE];
+        int fst, sfst, n_used;
+        expert_scan(tot, chunk, true, wsum, fst, sfst, n_used);
         base_s[e] = bse;
         first_s[e] = fst;
         sfirst_s[e] = sfst;

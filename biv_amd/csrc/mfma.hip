@@ -969,20 +969,6 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
                 }
             }
         };
-        auto step = [&](int h, const typename W::Step &w) {
-            if constexpr (W::BOTH) {
-                compute(h, std::integral_constant<int, 0>(), w);
-                compute(h, std::integral_constant<int, 1>(), w);
-            } else if (h & 1) {
-                compute(h >> 1, std::integral_constant<int, 1>(), w);
-            } else {
-                compute(h >> 1, std::integral_constant<int, 0>(), w);
-            }
-        };
-        // two steps per turn, loads one ahead (the last turn reloads its own
-        // step rather than branch: a branch in the loop body lets the
-        // compiler sink the chains' FMAs past it, keeping every MFMA result
-        // of a step live at once)
         static_assert(W::STEPS % 2 == 0, "steps");
         // step h of parity PAR (compile-time: a runtime parity would be a
         // branch in the loop body, past which the compiler sinks the chains'
