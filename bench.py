@@ -66,7 +66,7 @@ def stage_bytes(stage, U, T):
 TRAFFIC = {
     ("gate_up", 1): 20207131, ("gate_up", 5): 91705677, ("gate_up", 40): 430113924,
     ("down", 1): 10344203, ("down", 5): 46907741, ("down", 40): 217679560,
-    ("gate_up", 512): 709451776, ("down", 512): 371922944,
+    ("gate_up", 512): 697649152, ("down", 512): 365848576,
 }
 
 
