@@ -1067,6 +1067,39 @@ __global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
     const DevMat &M = shared ? a.sa : a.a;
     const int rows = M.rows;
     const int rw0 = rt * Q_ROWS_WG + wave * 16 * RT;
+    // this lane's weight words of group gq, per row tile
+    uint4 ql[RT][2][2], qh[RT][2];
+    int4 scv[RT][2];
+    float dsb[RT][2];
+    auto load_group = [&](int gq) {
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const size_t row = (size_t)e * rows + rw0 + 16 * r + n;
+            const uint8_t *base = M.q + row * (K / 256) * 192;
+            const uint4 *pl = reinterpret_cast<const uint4 *>(base);
+            const uint4 *ph = reinterpret_cast<const uint4 *>(base + (K / 256) * 128);
+#pragma unroll
+            for (int pi = 0; pi < 2; pi++)
+#pragma unroll
+                for (int w = 0; w < 2; w++) ql[r][pi][w] = pl[16 * gq + 8 * pi + 2 * kq + w];
+#pragma unroll
+            for (int w = 0; w < 2; w++) qh[r][w] = ph[8 * gq + 2 * kq + w];
+            // sub-scales of the group's 16 blocks: [pi][hsel] runs of K / 64
+            const int8_t *sc = reinterpret_cast<const int8_t *>(M.s + row * (K / 16));
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                // scv[r][c]: bytes [pi = c][hsel = 0 / 1][s = 8 gq .. + 7] as two int2 halves
+                const uint2 s0 = *reinterpret_cast<const uint2 *>(sc + (2 * c + 0) * (K / 64) + 8 * gq);
+                const uint2 s1 = *reinterpret_cast<const uint2 *>(sc + (2 * c + 1) * (K / 64) + 8 * gq);
+                scv[r][c] = make_int4((int)s0.x, (int)s0.y, (int)s1.x, (int)s1.y);
+            }
+            const uint16_t *dp = reinterpret_cast<const uint16_t *>(M.d + row * (K / 256) * 2);
+            dsb[r][0] = f16_to_f32(dp[2 * gq]);
+            dsb[r][1] = f16_to_f32(dp[2 * gq + 1]);
+        }
+    };
+    // the first group's weights go out before the staging waits
+    load_group(0);
     // stage the slot's input rows (as the Q8_0 down kernel)
     {
         constexpr int UPR = K / 16;
@@ -1093,35 +1126,7 @@ __global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
 #pragma unroll
         for (int r = 0; r < RT; r++) acc[t][r][0] = acc[t][r][1] = 0.0f;
     for (int gq = 0; gq < NQ; gq++) {
-        // this lane's weight words of the group, per row tile
-        uint4 ql[RT][2][2], qh[RT][2];
-        int4 scv[RT][2];
-        float dsb[RT][2];
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            const size_t row = (size_t)e * rows + rw0 + 16 * r + n;
-            const uint8_t *base = M.q + row * (K / 256) * 192;
-            const uint4 *pl = reinterpret_cast<const uint4 *>(base);
-            const uint4 *ph = reinterpret_cast<const uint4 *>(base + (K / 256) * 128);
-#pragma unroll
-            for (int pi = 0; pi < 2; pi++)
-#pragma unroll
-                for (int w = 0; w < 2; w++) ql[r][pi][w] = pl[16 * gq + 8 * pi + 2 * kq + w];
-#pragma unroll
-            for (int w = 0; w < 2; w++) qh[r][w] = ph[8 * gq + 2 * kq + w];
-            // sub-scales of the group's 16 blocks: [pi][hsel] runs of K / 64
-            const int8_t *sc = reinterpret_cast<const int8_t *>(M.s + row * (K / 16));
-#pragma unroll
-            for (int c = 0; c < 2; c++) {
-                // scv[r][c]: bytes [pi = c][hsel = 0 / 1][s = 8 gq .. + 7] as two int2 halves
-                const uint2 s0 = *reinterpret_cast<const uint2 *>(sc + (2 * c + 0) * (K / 64) + 8 * gq);
-                const uint2 s1 = *reinterpret_cast<const uint2 *>(sc + (2 * c + 1) * (K / 64) + 8 * gq);
-                scv[r][c] = make_int4((int)s0.x, (int)s0.y, (int)s1.x, (int)s1.y);
-            }
-            const uint16_t *dp = reinterpret_cast<const uint16_t *>(M.d + row * (K / 256) * 2);
-            dsb[r][0] = f16_to_f32(dp[2 * gq]);
-            dsb[r][1] = f16_to_f32(dp[2 * gq + 1]);
-        }
+        if (gq > 0) load_group(gq);
 #pragma unroll
         for (int bl = 0; bl < 16; bl++) { // block b = 16 gq + bl: half qq = 4 gq + bl / 4, quarter k = bl % 4
             const int qq = bl >> 2, k = bl & 3, pi = k & 1, hi = k >> 1;
