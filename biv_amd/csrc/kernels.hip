@@ -1442,8 +1442,13 @@ template <int K> struct Chain<T_Q8_0, K> {
 // of sub-block 2s + pi (quant.rs:1384-1423)
 template <int K> struct Chain<T_Q4K, K> {
     static constexpr int S = K / 64;
-    int w[S];
-    float ws[S];
+    // the nibbles of steps 2m (low) and 2m + 1 (high) of each byte in wp[m];
+    // per super-block its f32 d and the four sub-scales of this parity as
+    // bytes: half the registers of whole words and f32 scales, for more
+    // waves per SIMD
+    int wp[S / 2];
+    float ds[S / 4];
+    int scp[S / 4];
     __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l) { load_chunk(M, mrow, K, 0, pi, l); }
     __device__ inline void load_chunk(const DevMat &M, size_t mrow, int KF, int c, int pi, int l)
     {
@@ -1452,28 +1457,38 @@ template <int K> struct Chain<T_Q4K, K> {
 #pragma unroll
         for (int i = 0; i < S / 4; i++) {
             int4 v = q[i * 8 + l];
-            w[4 * i] = (int)(((unsigned)v.x >> sh) & 0x0F0F0F0Fu);
-            w[4 * i + 1] = (int)(((unsigned)v.y >> sh) & 0x0F0F0F0Fu);
-            w[4 * i + 2] = (int)(((unsigned)v.z >> sh) & 0x0F0F0F0Fu);
-            w[4 * i + 3] = (int)(((unsigned)v.w >> sh) & 0x0F0F0F0Fu);
+            const unsigned w0 = ((unsigned)v.x >> sh) & 0x0F0F0F0Fu, w1 = ((unsigned)v.y >> sh) & 0x0F0F0F0Fu;
+            const unsigned w2 = ((unsigned)v.z >> sh) & 0x0F0F0F0Fu, w3 = ((unsigned)v.w >> sh) & 0x0F0F0F0Fu;
+            wp[2 * i] = (int)(w0 | (w1 << 4));
+            wp[2 * i + 1] = (int)(w2 | (w3 << 4));
         }
         const int4 *hd = reinterpret_cast<const int4 *>(M.s + 16 * (mrow * (KF / 256) + (size_t)c * (K / 256)));
 #pragma unroll
         for (int i = 0; i < S / 4; i++) {
             const int4 h = hd[i];
-            const float d = __half2float(__ushort_as_half((unsigned short)(h.x & 0xFFFF)));
+            ds[i] = __half2float(__ushort_as_half((unsigned short)(h.x & 0xFFFF)));
+            unsigned packed = 0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int sb = 2 * j + pi;
                 int sc;
                 if (sb < 4) sc = byte_at(h, 4 + sb) & 63;
                 else sc = (byte_at(h, 4 + sb + 4) & 0xF) | ((byte_at(h, 4 + sb - 4) >> 6) << 4);
-                ws[4 * i + j] = d * (float)sc;
+                packed |= (unsigned)sc << (8 * j);
             }
+            scp[i] = (int)packed;
         }
     }
-    __device__ inline int partial(int s, int x) const { return dot4(w[s], x, 0); }
-    __device__ inline float wscale(int s) const { return ws[s]; }
+    __device__ inline int partial(int s, int x) const
+    {
+        const unsigned w = (unsigned)wp[s >> 1];
+        return dot4((int)((s & 1) ? (w >> 4) & 0x0F0F0F0Fu : w & 0x0F0F0F0Fu), x, 0);
+    }
+    // d * sc of the step's sub-block, the product the reference forms
+    __device__ inline float wscale(int s) const
+    {
+        return ds[s >> 2] * (float)(((unsigned)scp[s >> 2] >> (8 * (s & 3))) & 0xFF);
+    }
 };
 
 // Q6_K: lanes of madd(maddubs(q, x) - maddubs(32, x), sc), lanes 0-3 under
