@@ -191,9 +191,10 @@ int biv_hip_numerics(const biv_hip_ctx *ctx, char *buf, size_t len);
 size_t biv_hip_device_bytes(const biv_hip_ctx *ctx);
 
 /* Stage timing for measurement: while enabled, every forward records a HIP
- * event on the context's stream before each of its 6 launches (router with
- * the quantisation of h; route and dispatch sort; gate/up; quantisation of
- * the intermediate; down; combine) and after the last.
+ * event on the context's stream before each of its 6 stages (router with
+ * the quantisation of h, or pre-pass and router; route and dispatch sort;
+ * gate/up; quantisation of the intermediate; down; combine), a stage being
+ * one or more launches or none, and after the last.
  * biv_hip_stage_times waits for the stream, writes the summed milliseconds
  * per stage into ms[0..5] and the number of timed forwards, and forgets
  * them.  The reference times with wall clocks only
