@@ -1663,15 +1663,18 @@ constexpr size_t LONG_FULL_LDS = BIV_LONG_FULL_LDS; // LDS bytes up to which a w
 
 // FULL: every chunk of the workgroup's activation rows is staged in LDS
 // (dynamic, nc buffers) before the loop, so the loop only streams weights,
-// LPD chunks ahead in a ring of registers whose waits the compiler places.
+// LPD chunks ahead in a ring of registers whose waits the compiler places
+// (two for five tokens or more: their accumulators and staged operands
+// leave registers for fewer chunks, and the freed ones buy a wave per SIMD).
 #ifndef BIV_LONG_LPD
 #define BIV_LONG_LPD 4
 #endif
-constexpr int LPD = BIV_LONG_LPD;
+template <int XTT> constexpr int long_lpd() { return XTT >= 5 ? 2 : BIV_LONG_LPD; }
 
 template <int TY, bool GATEUP, int XTT, int WV>
 __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long_full(LongArgs a)
 {
+    constexpr int LPD = long_lpd<XTT>();
     constexpr int K = LK, S = K / 64, ROW16 = K / 16 + K / 128, NTH = WV * WAVE;
     constexpr bool BF = TY == T_BF16;
     constexpr int PIECES = BF ? XTT * K / 4 : XTT * ROW16; // 16-byte pieces of one chunk's rows (XTT rows)
