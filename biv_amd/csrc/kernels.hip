@@ -1664,17 +1664,22 @@ constexpr size_t LONG_FULL_LDS = BIV_LONG_FULL_LDS; // LDS bytes up to which a w
 // FULL: every chunk of the workgroup's activation rows is staged in LDS
 // (dynamic, nc buffers) before the loop, so the loop only streams weights,
 // LPD chunks ahead in a ring of registers whose waits the compiler places
-// (two for five tokens or more: their accumulators and staged operands
-// leave registers for fewer chunks, and the freed ones buy a wave per SIMD).
+// (gate/up: two for five tokens or more, whose accumulators and staged
+// operands leave registers for fewer chunks, the freed ones buying a wave per
+// SIMD; down: eight, its 4-row waves being too few for more than one wave
+// per SIMD anyway, so that registers go to bytes in flight).
 #ifndef BIV_LONG_LPD
 #define BIV_LONG_LPD 4
 #endif
-template <int XTT> constexpr int long_lpd() { return XTT >= 5 ? 2 : BIV_LONG_LPD; }
+#ifndef BIV_LONG_LPD_DN
+#define BIV_LONG_LPD_DN 8
+#endif
+template <int XTT, bool GATEUP> constexpr int long_lpd() { return GATEUP ? (XTT >= 5 ? 2 : BIV_LONG_LPD) : BIV_LONG_LPD_DN; }
 
 template <int TY, bool GATEUP, int XTT, int WV>
 __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long_full(LongArgs a)
 {
-    constexpr int LPD = long_lpd<XTT>();
+    constexpr int LPD = long_lpd<XTT, GATEUP>();
     constexpr int K = LK, S = K / 64, ROW16 = K / 16 + K / 128, NTH = WV * WAVE;
     constexpr bool BF = TY == T_BF16;
     constexpr int PIECES = BF ? XTT * K / 4 : XTT * ROW16; // 16-byte pieces of one chunk's rows (XTT rows)
