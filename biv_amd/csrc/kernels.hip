@@ -1620,6 +1620,42 @@ __device__ inline float q4k_mins(const DevMat &M, size_t mrow, const float *xs, 
     return mins;
 }
 
+// q4k_mins by the 16 lanes of a group (lane ln of the group, every lane
+// calling it for the same row and input row): lane ln forms the terms s =
+// ln, ln + 16, ... (the loads of all terms in flight at once, where one lane
+// would wait on them in turn), then every lane adds them in index order,
+// read across the group, so the sum is q4k_mins's to the bit.
+template <int K>
+__device__ inline float q4k_mins_group(const DevMat &M, size_t mrow, const float *xs, size_t xrow, int ln)
+{
+    constexpr int S = K / 64;          // sub-block pairs: the terms
+    constexpr int R = (S + 15) / 16;   // terms per lane
+    const int4 *hd = reinterpret_cast<const int4 *>(M.s + 16 * (mrow * (K / 256)));
+    const float *sr = xs + xrow * (K / 32);
+    float term[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int s = ln + 16 * r;
+        term[r] = 0.0f;
+        if (s < S) {
+            const int4 h = hd[s >> 2];
+            const int j = s & 3;
+            const float dmin = __half2float(__ushort_as_half((unsigned short)((unsigned)h.x >> 16)));
+            const int sa = 2 * j, sb = 2 * j + 1;
+            const int ma = sa < 4 ? byte_at(h, 4 + sa + 4) & 63
+                                  : (byte_at(h, 4 + sa + 4) >> 4) | ((byte_at(h, 4 + sa) >> 6) << 4);
+            const int mb = sb < 4 ? byte_at(h, 4 + sb + 4) & 63
+                                  : (byte_at(h, 4 + sb + 4) >> 4) | ((byte_at(h, 4 + sb) >> 6) << 4);
+            term[r] = dmin * ((float)ma * sr[lay::q8_scale(K, 2 * s)] + (float)mb * sr[lay::q8_scale(K, 2 * s + 1)]);
+        }
+    }
+    const int base = (int)(threadIdx.x & 63) & ~15;
+    float mins = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; s++) mins = mins + __shfl(term[s / 16], base + (s % 16));
+    return mins;
+}
+
 // The Q4_K mins of chunk c of a row of KF (q4k_mins over that chunk's
 // sub-block pairs), added to `mins` in the reference's order.
 template <int K>
@@ -2122,11 +2158,7 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
                 t = t + __shfl_xor(t, 4);           // the two 128-bit halves
                 t = t + __shfl_xor(t, 2);           // movehl
                 t = t + __shfl_xor(t, 1);           // movehdup
-                if (TY == T_Q4K) {
-                    float mins = 0.0f;
-                    if (ln == 0) mins = q4k_mins<K>(M, (size_t)e * rows + (row_ok ? row : 0), a.xs, xrow);
-                    t = t - __shfl(mins, lane & ~15);
-                }
+                if (TY == T_Q4K) t = t - q4k_mins_group<K>(M, (size_t)e * rows + (row_ok ? row : 0), a.xs, xrow, ln);
                 if (GATEUP) {
                     const float up = __shfl_xor(t, 16);
                     if (m == 0 && ln == 0 && row_ok) a.out[orow * rows + row] = silu_mul(t, up);
