@@ -1623,8 +1623,9 @@ __device__ inline float q4k_mins(const DevMat &M, size_t mrow, const float *xs, 
 // q4k_mins by the 16 lanes of a group (lane ln of the group, every lane
 // calling it for the same row and input row): lane ln forms the terms s =
 // ln, ln + 16, ... (the loads of all terms in flight at once, where one lane
-// would wait on them in turn), then every lane adds them in index order,
-// read across the group, so the sum is q4k_mins's to the bit.
+// would wait on them in turn), then the group's first lane adds them in
+// index order, so its sum is q4k_mins's to the bit (the other lanes' are
+// not: only the first lane's result is used).
 template <int K>
 __device__ inline float q4k_mins_group(const DevMat &M, size_t mrow, const float *xs, size_t xrow, int ln)
 {
@@ -1649,11 +1650,21 @@ __device__ inline float q4k_mins_group(const DevMat &M, size_t mrow, const float
             term[r] = dmin * ((float)ma * sr[lay::q8_scale(K, 2 * s)] + (float)mb * sr[lay::q8_scale(K, 2 * s + 1)]);
         }
     }
-    const int base = (int)(threadIdx.x & 63) & ~15;
+    // the sum in index order in the group's first lane: its term r of lane
+    // k reaches it through k single-lane rotations within the 16-lane row
+    // (DPP row_shl:1, no LDS)
     float mins = 0.0f;
 #pragma unroll
-    for (int s = 0; s < S; s++) mins = mins + __shfl(term[s / 16], base + (s % 16));
-    return mins;
+    for (int r = 0; r < R; r++) {
+        float x = term[r];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (16 * r + k >= S) break;
+            mins = mins + x;
+            if (k < 15) x = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x101, 0xF, 0xF, false));
+        }
+    }
+    return mins; // in the group's first lane
 }
 
 // The Q4_K mins of chunk c of a row of KF (q4k_mins over that chunk's
