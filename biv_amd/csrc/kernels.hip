@@ -81,9 +81,16 @@ template <int N> __device__ inline void ld_words(const void *p, int (&out)[N])
 // (srow may be null); generic pointers, so the row may be in LDS.
 __device__ inline void quant_block_at(const float (&v)[32], int K, int b, int *qrow, float *drow, float *srow)
 {
-    float amax = 0.0f;
+    // the largest magnitude as a tree: max is exact, so any order gives the
+    // sequential loop's value (NaNs skipped by fmaxf alike; 0 if all are)
+    float m[16];
 #pragma unroll
-    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
+    for (int j = 0; j < 16; j++) m[j] = fmaxf(fabsf(v[2 * j]), fabsf(v[2 * j + 1]));
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int j = 0; j < w; j++) m[j] = fmaxf(m[j], m[j + w]);
+    const float amax = fmaxf(0.0f, m[0]);
     const float db = amax / 127.0f;
     const float id = db != 0.0f ? 1.0f / db : 0.0f;
     int sum = 0;
@@ -2337,7 +2344,12 @@ __global__ __launch_bounds__(DC_WAVES *WAVE) void k_down_combine(DcArgs a)
         const bool sh = h.x < 0;
         c.load(sh ? a.sa : a.a, (size_t)(sh ? 0 : h.x) * rows + r, pi, l);
     };
-    // the first weight rows go out before the intermediate is staged
+    // the thread's first block of the intermediate goes out first, then the
+    // first weight rows: loads complete in order, so the block's
+    // quantisation runs while the weights are still arriving
+    const int nblk = R * (K / 32);
+    float v0[32];
+    if (tid < nblk) load32(a.xf + (size_t)(tid / (K / 32)) * K + 32 * (tid % (K / 32)), v0);
     constexpr int DC_D = dc_depth<K>();
     Chain<TY, K> wc[DC_D];
 #pragma unroll
@@ -2357,7 +2369,10 @@ __global__ __launch_bounds__(DC_WAVES *WAVE) void k_down_combine(DcArgs a)
     const float cres = a.add && cmine ? *cpo : 0.0f;
     if (tid < 32) tab[tid] = exp_tab_g[tid];
     // the intermediate, quantised into LDS: one 32-element block per thread and turn
-    for (int b = tid; b < R * (K / 32); b += NTH) {
+    if (tid < nblk)
+        quant_block_at(v0, K, tid % (K / 32), reinterpret_cast<int *>(&stage[(tid / (K / 32)) * ROW16]),
+                       reinterpret_cast<float *>(&stage[(tid / (K / 32)) * ROW16 + K / 16]), nullptr);
+    for (int b = tid + NTH; b < nblk; b += NTH) {
         const int r = b / (K / 32), bb = b - r * (K / 32);
         float v[32];
         load32(a.xf + (size_t)r * K + 32 * bb, v);
