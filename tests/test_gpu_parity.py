@@ -453,6 +453,18 @@ def test_bf16_full_size_4096(orc, engine):
     _full_size(orc, moe, layer, synth.make_tokens(4096, 4096))
 
 
+@pytest.mark.parametrize("E", [512, 1024])
+def test_kquant_widths(orc, engine, E):
+    """Q4_K gate/up and Q6_K down at widths 512 and 1024 (K = 512 / 1024
+    chains: the Q4_K mins over 8 / 16 sub-block pairs, summed by the row's
+    16 lanes), decode sizes, bit-identical to the oracle."""
+    print(f"case kquant widths E={E}", flush=True)
+    layer, moe = layer_for(engine, seed=43, n_embd=E, n_ff=E, n_ff_sh=E, n_expert=16, types=(Q4K, Q4K, Q6K))
+    for T in (1, 5):
+        h = synth.make_tokens(600 + T, T, n_embd=E, offsets=T > 1)
+        full_parity(orc, engine, layer, moe, h)
+
+
 @pytest.mark.parametrize("T", [1, 5, 64, 300])
 def test_other_widths(orc, engine, T):
     """A layer of other widths: n_embd 1024, n_ff 1024, 64 experts (the
