@@ -582,7 +582,7 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     // BF16 gate/up on the matrix cores from the pre-pass's bf16 halves of h
     const bool prep_split = mf_gu && T >= biv::prep_min_t();
     if (prep_split) {
-        ra.xh = reinterpret_cast<uint4 *>(s.xh);
+        ra.xh = reinterpret_cast<uint4 *>(s.xh); // the pre-pass then skips the Q8 of h
         ra.xl = reinterpret_cast<uint4 *>(s.xl);
     }
     if (norm_w) {

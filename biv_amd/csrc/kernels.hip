@@ -702,11 +702,12 @@ __device__ inline void wave_lds_sync()
 //     written to hn;
 //   the shared expert's gate logit gate_inp . h in dot_f32's order
 //     (quant.rs:1177-1207), chain L in lane L, then the tree;
-//   the Q8 for the experts of the (normalised) row: it goes through LDS
-//     (32-element blocks at a 36-float pitch) so that lane b quantises
-//     block b;
-//   with xh, the bf16 hi / lo halves of the row for BF16 experts (from the
-//     LDS copy, as k_split_bf16 forms them).
+//   without xh, the Q8 for the experts of the (normalised) row: it goes
+//     through LDS (32-element blocks at a 36-float pitch) so that lane b
+//     quantises block b;
+//   with xh, instead, the bf16 hi / lo halves of the row for BF16 experts
+//     (from the LDS copy, as k_split_bf16 forms them): nothing reads the
+//     Q8 of h when every gate/up takes the halves.
 // Lanes 32-63 repeat the chains of lanes 0-31 (the shuffle tree stays within
 // each half); each half writes half of the row (to hn and LDS).  The norm
 // weights and the gate row, the chains' operands, are staged in LDS once per
@@ -768,7 +769,7 @@ template <int NS> __global__ __launch_bounds__(64 * PREP_TOK) void k_prep(Router
     for (int k = 0; k < NS; k++)
         if ((k < NS / 2) == (hi == 0)) r[k * PREP_PITCH + L] = v[k];
     wave_lds_sync();
-    if (lane < NS)
+    if (!a.xh && lane < NS)
         quant_block_lds(reinterpret_cast<const float4 *>(r + lane * PREP_PITCH), E, lane,
                         reinterpret_cast<int *>(a.xq + (size_t)t * E), a.xd + (size_t)t * (E / 32),
                         a.xs + (size_t)t * (E / 32));
