@@ -582,9 +582,12 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     // BF16 gate/up on the matrix cores from the pre-pass's bf16 halves of h
     const bool prep_split = mf_gu && T >= biv::prep_min_t();
     if (prep_split) {
-        ra.xh = reinterpret_cast<uint4 *>(s.xh); // the pre-pass then skips the Q8 of h
+        ra.xh = reinterpret_cast<uint4 *>(s.xh);
         ra.xl = reinterpret_cast<uint4 *>(s.xl);
     }
+    // BF16 gate/up (routed and shared) read h as f32 or as its bf16 halves:
+    // nothing reads the Q8 of h, so the router launch leaves it out
+    if (m->gate->m.ty == biv::T_BF16 && (!has_shared || m->sg->m.ty == biv::T_BF16)) ra.xq = nullptr;
     if (norm_w) {
         if (h == s.h_stage) return fail(ctx, BIV_HIP_E_INVALID, "post_norm input aliases its output");
         h = s.h_stage; // every later use of h takes the normalised rows

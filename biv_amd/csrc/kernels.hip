@@ -194,7 +194,9 @@ template <int NS, int TC, int NTH = 256> __global__ __launch_bounds__(NTH) void 
     const float *__restrict__ h = a.h;
     const int n_expert = a.n_expert, T = a.T;
     // Workgroups past the row groups quantise h for the experts (Q8 rows in
-    // the chain layout): one 32-element block per thread and turn.
+    // the chain layout): one 32-element block per thread and turn.  With no
+    // xq (BF16 layers, which read h as f32) there are none, or, with the
+    // post_norm, they write hn only.
     const int n_rw = (n_expert + 1 + RPW - 1) / RPW;
     if ((int)blockIdx.x >= n_rw && a.norm_w) {
         // post_norm first: a half wave per token forms its RMS scale (the
@@ -226,7 +228,7 @@ template <int NS, int TC, int NTH = 256> __global__ __launch_bounds__(NTH) void 
                     v[4 * j + 3] = v[4 * j + 3] * (scale * w.w);
                     o4[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
                 }
-                quant_block(v, E, t, b, a.xq, a.xd, a.xs);
+                if (a.xq) quant_block(v, E, t, b, a.xq, a.xd, a.xs);
             }
         }
         return;
@@ -702,12 +704,11 @@ __device__ inline void wave_lds_sync()
 //     written to hn;
 //   the shared expert's gate logit gate_inp . h in dot_f32's order
 //     (quant.rs:1177-1207), chain L in lane L, then the tree;
-//   without xh, the Q8 for the experts of the (normalised) row: it goes
+//   with xq, the Q8 for the experts of the (normalised) row: it goes
 //     through LDS (32-element blocks at a 36-float pitch) so that lane b
-//     quantises block b;
-//   with xh, instead, the bf16 hi / lo halves of the row for BF16 experts
-//     (from the LDS copy, as k_split_bf16 forms them): nothing reads the
-//     Q8 of h when every gate/up takes the halves.
+//     quantises block b (BF16 layers, which never read it, pass none);
+//   with xh, the bf16 hi / lo halves of the row for BF16 experts (from the
+//     LDS copy, as k_split_bf16 forms them).
 // Lanes 32-63 repeat the chains of lanes 0-31 (the shuffle tree stays within
 // each half); each half writes half of the row (to hn and LDS).  The norm
 // weights and the gate row, the chains' operands, are staged in LDS once per
@@ -769,7 +770,7 @@ template <int NS> __global__ __launch_bounds__(64 * PREP_TOK) void k_prep(Router
     for (int k = 0; k < NS; k++)
         if ((k < NS / 2) == (hi == 0)) r[k * PREP_PITCH + L] = v[k];
     wave_lds_sync();
-    if (!a.xh && lane < NS)
+    if (a.xq && lane < NS)
         quant_block_lds(reinterpret_cast<const float4 *>(r + lane * PREP_PITCH), E, lane,
                         reinterpret_cast<int *>(a.xq + (size_t)t * E), a.xd + (size_t)t * (E / 32),
                         a.xs + (size_t)t * (E / 32));
@@ -2556,7 +2557,7 @@ hipError_t launch_router(const RouterArgs &a0, hipStream_t st)
     }
     const int rows = a.n_expert + 1;
     // quantisation workgroups beside the row groups: about one block per thread
-    const int qblocks = a.T * (a.E / 32);
+    const int qblocks = a.xq || a.norm_w ? a.T * (a.E / 32) : 0;
     // 8 rows per workgroup; tokens split over grid.y in chunks of TC (32 KB of
     // LDS, 64 KB past 2 TC tokens); batches of 2..64 tokens in chunks of TC / 4
     // (up to 16 tokens) or TC / 2: more workgroups, shorter chains each
