@@ -186,9 +186,17 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     auto lds_load = [](const uint4 *src, uint4 *dst_wave) {
         __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst_wave, 16, 0, 0);
     };
-    auto issue = [&](int s, uint4 *sA, uint4 *sB) {
+    // A load q of a thread covers pairs 128 (q & 1) .. + 127 of half q >> 1
+    // (for every wave alike): a slot of at most 128 pairs (HALF) leaves out
+    // the odd ones, which would only load its last pair again.  (Leaving out
+    // each wave's loads that hold no pair of the slot, down to all of them,
+    // measured no faster.)
+    static_assert(A_SLOTS / NTH == 4 && NTH / SK == 128, "A loads by pair halves");
+    auto issue = [&](int s, uint4 *sA, uint4 *sB, auto half_c) {
+        constexpr bool HALF = decltype(half_c)::value;
 #pragma unroll
-        for (int q = 0; q < A_SLOTS / NTH; q++) lds_load(srcA[q] + s * SK + swA[q], sA + NTH * q + 64 * wave);
+        for (int q = 0; q < A_SLOTS / NTH; q++)
+            if (!HALF || !(q & 1)) lds_load(srcA[q] + s * SK + swA[q], sA + NTH * q + 64 * wave);
 #pragma unroll
         for (int q = 0; q < B_SLOTS / NTH; q++) lds_load(srcB[q] + s * SK + swB[q], sB + NTH * q + 64 * wave);
     };
@@ -234,36 +242,43 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         }
     };
     // three buffers, loads two stages ahead: stage s is in buffer s % 3
-    constexpr int NLD = A_SLOTS / NTH + B_SLOTS / NTH; // loads of a stage, per thread
-    // s_waitcnt immediates: vmcnt <= NLD (or 0) and lgkmcnt 0 (this wave's
-    // LDS reads of the buffer the next loads overwrite are done)
-    constexpr int WAIT_ONE_STAGE = (NLD & 15) | ((NLD >> 4) << 14) | (7 << 4);
-    constexpr int WAIT_NONE_LEFT = 7 << 4;
-    auto step = [&](int s, const uint4 *__restrict__ cA, const uint4 *__restrict__ cB, uint4 *__restrict__ nA,
-                    uint4 *__restrict__ nB) {
-        // this thread's loads of stage s are in (stage s + 1's may be in
-        // flight); after the barrier every thread's are, and every wave is
-        // done with stage s - 1, whose buffer stage s + 2 takes
-        if (s + 1 < NS) __builtin_amdgcn_s_waitcnt(WAIT_ONE_STAGE);
-        else __builtin_amdgcn_s_waitcnt(WAIT_NONE_LEFT);
-        // a raw s_barrier (the compiler's barrier would wait for every load)
-        // between compiler fences, so no LDS access moves across it
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        if (s + 2 < NS) issue(s + 2, nA, nB);
-        compute(cA, cB);
+    auto run = [&](auto half_c) {
+        constexpr bool HALF = decltype(half_c)::value;
+        // loads of a stage, per thread
+        constexpr int NLD = (HALF ? A_SLOTS / NTH / 2 : A_SLOTS / NTH) + B_SLOTS / NTH;
+        // s_waitcnt immediates: vmcnt <= NLD (or 0) and lgkmcnt 0 (this
+        // wave's LDS reads of the buffer the next loads overwrite are done)
+        constexpr int WAIT_ONE_STAGE = (NLD & 15) | ((NLD >> 4) << 14) | (7 << 4);
+        constexpr int WAIT_NONE_LEFT = 7 << 4;
+        auto step = [&](int s, const uint4 *__restrict__ cA, const uint4 *__restrict__ cB, uint4 *__restrict__ nA,
+                        uint4 *__restrict__ nB) {
+            // this thread's loads of stage s are in (stage s + 1's may be in
+            // flight); after the barrier every thread's are, and every wave
+            // is done with stage s - 1, whose buffer stage s + 2 takes
+            if (s + 1 < NS) __builtin_amdgcn_s_waitcnt(WAIT_ONE_STAGE);
+            else __builtin_amdgcn_s_waitcnt(WAIT_NONE_LEFT);
+            // a raw s_barrier (the compiler's barrier would wait for every
+            // load) between compiler fences, so no LDS access moves across it
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (s + 2 < NS) issue(s + 2, nA, nB, half_c);
+            compute(cA, cB);
+        };
+        issue(0, sA0, sB0, half_c);
+        if (NS > 1) issue(1, sA1, sB1, half_c);
+        int s = 0;
+        for (; s + 3 <= NS; s += 3) {
+            step(s, sA0, sB0, sA2, sB2);
+            step(s + 1, sA1, sB1, sA0, sB0);
+            step(s + 2, sA2, sB2, sA1, sB1);
+        }
+        if (s < NS) step(s, sA0, sB0, sA2, sB2);
+        if (s + 1 < NS) step(s + 1, sA1, sB1, sA0, sB0);
     };
-    issue(0, sA0, sB0);
-    if (NS > 1) issue(1, sA1, sB1);
-    int s = 0;
-    for (; s + 3 <= NS; s += 3) {
-        step(s, sA0, sB0, sA2, sB2);
-        step(s + 1, sA1, sB1, sA0, sB0);
-        step(s + 2, sA2, sB2, sA1, sB1);
-    }
-    if (s < NS) step(s, sA0, sB0, sA2, sB2);
-    if (s + 1 < NS) step(s + 1, sA1, sB1, sA0, sB0);
+    // uniform over the workgroup (compute reads only the pairs below cnt)
+    if (cnt <= TOK_TILE / 2) run(std::true_type());
+    else run(std::false_type());
     // the exp table in LDS for the SwiGLU
     __shared__ uint64_t tab[GATEUP ? 32 : 1];
     if (GATEUP) {
