@@ -1544,7 +1544,14 @@ template <int K> struct Chain<T_Q6K, K> {
         const int qq = s >> 1, hi = s & 1, k = pi_ + 2 * hi;
         const unsigned lo = hi ? (((unsigned)ql[qq] >> 4) & 0x0F0F0F0Fu) : ((unsigned)ql[qq] & 0x0F0F0F0Fu);
         const unsigned hb = (((unsigned)qh[qq] >> (2 * k)) & 0x03030303u) << 4;
-        return sc[s] * (dot4((int)(lo | hb), x, 0) - 32 * dot4(0x01010101, x, 0));
+        // a 24-bit product (full rate; a 32-bit multiply is quarter rate):
+        // |dot| <= 4 * 63 * 128 + 32 * 512 and sc is int8, so it is the same
+        // integer.  In asm: for __mul24 the compiler sign-extends both
+        // operands and, in some kernels, still emits the 32-bit multiply.
+        const int d = dot4((int)(lo | hb), x, 0) - 32 * dot4(0x01010101, x, 0);
+        int r;
+        asm("v_mul_i32_i24 %0, %1, %2" : "=v"(r) : "v"(sc[s]), "v"(d));
+        return r;
     }
     __device__ inline float wscale(int s) const { return dd[s >> 2]; }
 };

@@ -361,16 +361,22 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
                     }
         }
     } else {
+        // pair ti's row starts (beg + ti) * rows floats in: one 64-bit base
+        // per pair block and 32-bit offsets (j / 4) * 8 rows + (j % 4) rows,
+        // not a 64-bit multiply per store
+        const int r1 = rows, r8 = 8 * rows;
 #pragma unroll
-        for (int tb = 0; tb < 2; tb++)
+        for (int tb = 0; tb < 2; tb++) {
+            const int t0 = wt * 64 + tb * 32 + 4 * kg;
+            float *ob = a.out + (size_t)(beg + t0) * rows + r0 + wr * 32 * RB + li;
 #pragma unroll
             for (int rb = 0; rb < RB; rb++)
 #pragma unroll
                 for (int j = 0; j < 16; j++) {
-                    const int ti = wt * 64 + tb * 32 + (j / 4) * 8 + 4 * kg + (j % 4);
-                    const int row = r0 + wr * 32 * RB + rb * 32 + li;
-                    if (ti < cnt) a.out[(size_t)(beg + ti) * rows + row] = acc[tb][rb][0][j];
+                    const int dt = (j / 4) * 8 + (j % 4);
+                    if (t0 + dt < cnt) ob[(j / 4) * r8 + (j % 4) * r1 + rb * 32] = acc[tb][rb][0][j];
                 }
+        }
     }
 }
 
@@ -1180,7 +1186,10 @@ __global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
                 for (int r = 0; r < RT; r++) {
                     const i32x4 z = {0, 0, 0, 0};
                     const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xo, wo[r], z, 0, 0, 0);
-                    const int is0 = sc0[r] * d[0] + sc1[r] * d[1], is1 = sc0[r] * d[2] + sc1[r] * d[3];
+                    // 24-bit products (full rate; |dot16| <= 16 * 128 * 32,
+                    // sub-scales int8): the same integers as 32-bit ones
+                    const int is0 = __mul24(sc0[r], d[0]) + __mul24(sc1[r], d[1]);
+                    const int is1 = __mul24(sc0[r], d[2]) + __mul24(sc1[r], d[3]);
                     const float dd = dsb[r][qq >> 1];
                     acc[t][r][0] = __builtin_fmaf((float)is0, dd * dx.x, acc[t][r][0]);
                     acc[t][r][1] = __builtin_fmaf((float)is1, dd * dx.y, acc[t][r][1]);
