@@ -847,6 +847,7 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
         // constant: it picks the chain accumulators)
         auto compute = [&](int g, auto pi_c, const typename W::Step &w) {
             constexpr int pi = decltype(pi_c)::value;
+            f16x8 wo_next; // block j + 1's first operand, formed during block j
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int b = 8 * g + pi + 2 * j;
@@ -935,14 +936,14 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
                 const float dw = W::scale(w, pi, j);
                 const int sidx = lay::q8_scale(K, b);
                 float sb[NT][4];
-#pragma unroll
-                for (int t = 0; t < NT; t++) {
+                auto scales = [&](int t) {
                     const float4 dx = *reinterpret_cast<const float4 *>(xd_s + sidx * DSTR + t * 8 + kg * 4);
                     sb[t][0] = dw * dx.x;
                     sb[t][1] = dw * dx.y;
                     sb[t][2] = dw * dx.z;
                     sb[t][3] = dw * dx.w;
-                }
+                };
+                scales(0); // (the second tile's: after the first MFMA)
                 const int jo = (j % GU_AJ) * NM; // this block's A operands
                 auto mfma = [&](int m, const f16x8 &wo) {
                     const f32x16 z = {};
@@ -965,15 +966,30 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
                         }
                     }
                 };
-                // each half's weight operand converted just before its MFMAs;
                 // one MFMA result live at a time (issuing the next MFMA before
-                // the FMAs of the last measured slower)
+                // the FMAs of the last measured slower); independent work goes
+                // between an MFMA and the FMAs that wait for its result: after
+                // the block's first MFMA the second half's weight operand and
+                // the second tile's scales, after its last the next block's
+                // first operand (Q8_0 at T = 512 256-259 -> 251-254 us, Q4_K
+                // at T = 2048 832-837 -> 821 us)
+                {
+                    const f16x8 wo0 = j > 0 ? wo_next : W::operand(w, pi, j, 0);
+                    const f32x16 d0 = mfma(0, wo0);
+                    const f16x8 wo1 = W::operand(w, pi, j, 1);
+                    if constexpr (NT == 2) scales(1);
+                    chains(0, d0);
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int hh = 0; hh < 2; hh++) {
-                    const f16x8 wo = W::operand(w, pi, j, hh);
+                    for (int t = 1; t < NT; t++) {
+                        chains(t, mfma(t, wo0));
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
 #pragma unroll
                     for (int t = 0; t < NT; t++) {
-                        chains(hh * NT + t, mfma(hh * NT + t, wo));
+                        const f32x16 d = mfma(NT + t, wo1);
+                        if (t == NT - 1 && j < 3) wo_next = W::operand(w, pi, j + 1, 0);
+                        chains(NT + t, d);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
