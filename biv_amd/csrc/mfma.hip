@@ -847,7 +847,9 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
         // constant: it picks the chain accumulators)
         auto compute = [&](int g, auto pi_c, const typename W::Step &w) {
             constexpr int pi = decltype(pi_c)::value;
-            f16x8 wo_next; // block j + 1's first operand, formed during block j
+            f16x8 wo_next;      // block j + 1's first operand, formed during block j
+            float sb_next[4];   // (Q8_0, two tiles) block j + 1's tile-0 scales, likewise
+            float4 dx_next;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int b = 8 * g + pi + 2 * j;
@@ -943,7 +945,15 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
                     sb[t][2] = dw * dx.z;
                     sb[t][3] = dw * dx.w;
                 };
-                scales(0); // (the second tile's: after the first MFMA)
+                // (the second tile's after the first MFMA; with two tiles,
+                // Q8_0 forms the next block's tile-0 scales during this one)
+                constexpr bool SB_AHEAD = !Q4K && NT == 2;
+                if (SB_AHEAD && j > 0) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) sb[0][q] = sb_next[q];
+                } else {
+                    scales(0);
+                }
                 const int jo = (j % GU_AJ) * NM; // this block's A operands
                 auto mfma = [&](int m, const f16x8 &wo) {
                     const f32x16 z = {};
@@ -982,12 +992,22 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                     for (int t = 1; t < NT; t++) {
-                        chains(t, mfma(t, wo0));
+                        const f32x16 d = mfma(t, wo0);
+                        if (SB_AHEAD && j < 3)
+                            dx_next = *reinterpret_cast<const float4 *>(xd_s + lay::q8_scale(K, b + 2) * DSTR + kg * 4);
+                        chains(t, d);
                         __builtin_amdgcn_sched_barrier(0);
                     }
 #pragma unroll
                     for (int t = 0; t < NT; t++) {
                         const f32x16 d = mfma(NT + t, wo1);
+                        if (SB_AHEAD && t == 0 && j < 3) {
+                            const float dwn = W::scale(w, pi, j + 1);
+                            sb_next[0] = dwn * dx_next.x;
+                            sb_next[1] = dwn * dx_next.y;
+                            sb_next[2] = dwn * dx_next.z;
+                            sb_next[3] = dwn * dx_next.w;
+                        }
                         if (t == NT - 1 && j < 3) wo_next = W::operand(w, pi, j + 1, 0);
                         chains(NT + t, d);
                         __builtin_amdgcn_sched_barrier(0);
