@@ -4,8 +4,9 @@
  * The library replaces, for one GPU, the MoE block that biv computes on the
  * CPU in Model::moe (engine/src/model.rs:860-898) and on Metal in
  * MetalEngine::encode_moe (engine/src/metal/mod.rs:2138-2266).  A Rust
- * `hip` backend binds these functions through `extern "C"`; the binding a
- * maintainer adds is shown in INTEGRATION.md.
+ * `hip` backend binds these functions through `extern "C"` declarations of
+ * the same names and argument types (pointers as *const / *mut, sizes as
+ * i32 / usize), next to the engine's existing backends.
  *
  * Conventions
  *  - Every function returns 0 on success and a negative BIV_HIP_E_* code on
