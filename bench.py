@@ -60,9 +60,11 @@ def stage_bytes(stage, U, T):
     return 0
 
 
-# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
-# (scaled by a copy kernel of known size: x2.0 and x1.0) on this workload:
-# profiles/moe_layer_q8_0_hbm_traffic.md.  Keyed by (stage, T).
+# HBM bytes per launch of the dominant kernel, not measured in this run: the
+# figures of rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over the same
+# workload (scaled by a copy kernel of known size: x2.0 and x1.0), committed
+# with their commands in TRAFFIC_SOURCE.  Keyed by (stage, T).
+TRAFFIC_SOURCE = "profiles/moe_layer_q8_0_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)"
 TRAFFIC = {
     ("gate_up", 1): 20207131, ("gate_up", 5): 91705677, ("gate_up", 40): 430113924,
     ("down", 1): 10344203, ("down", 5): 46907741, ("down", 40): 217679560,
@@ -106,35 +108,40 @@ def bench_gpu(eng, moes, layer, T, steps, warmup, torch):
         evs[i + 1].record()
     torch.cuda.synchronize()
     per = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]) * 1e3
-    # a second timed region with an event around every stage, for the
-    # per-kernel roofline (events add small gaps, so not the headline)
-    eng.set_timing(True)
-    for i in range(steps):
-        moes[i % L].forward_device(h_dev.data_ptr(), T, out_dev.data_ptr())
-    stage_ms, n = eng.stage_times()
-    eng.set_timing(False)
-    stage_us = {k: 1e3 * v / n for k, v in stage_ms.items()}
+    # each stage's launches alone, back to back over the layer copies (a
+    # kernel time, as rocprof's, with no event between stages); a stage with
+    # no launch at this T is null (T <= 16: the intermediate is quantised
+    # inside the down + combine launch, which the "down" stage is)
+    stage_us = {}
+    for st in STAGE_NAMES:
+        us = 1e3 * eng.time_stage(moes, h_dev.data_ptr(), T, out_dev.data_ptr(), st, steps)
+        stage_us[st] = us if us >= EMPTY_STAGE_US else None
     B = layer_bytes(U, T)
     res = {
         "T": T, "U": U, "us_per_layer": round(ms * 1e3, 3), "tokens_per_s": round(T / (ms * 1e-3), 1),
         "layer_GBps": round(B / (ms * 1e-3) / 1e9, 1), "layer_hbm_frac": round(B / (ms * 1e-3) / HBM_PEAK, 4),
         "us_median": round(float(np.median(per)), 3), "us_p10": round(float(np.percentile(per, 10)), 3),
         "us_p90": round(float(np.percentile(per, 90)), 3),
-        "stage_us": {k: round(v, 3) for k, v in stage_us.items()},
+        "stage_us": {k: (round(v, 3) if v is not None else None) for k, v in stage_us.items()},
         "wall_s": round(wall, 3),
     }
     if T >= 64:
         res["mfma"] = mfma_block(T, ms)
     # the dominant kernel alone: launched back to back over the layer copies
     # (the stage events above add a dispatch gap to every stage)
-    dom = max(("gate_up", "down", "router"), key=lambda s: stage_us[s])
-    kern_us = 1e3 * eng.time_stage(moes, h_dev.data_ptr(), T, out_dev.data_ptr(), dom, steps)
+    dom = max(("gate_up", "down", "router"), key=lambda s: stage_us[s] or 0.0)
+    kern_us = stage_us[dom]
     dbytes = stage_bytes(dom, U, T)
     ach = dbytes / (kern_us * 1e-6) / 1e9
     res["roofline"] = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK / 1e9,
                        "unit": "GB/s", "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": TRAFFIC.get((dom, T)),
+                       "traffic_source": TRAFFIC_SOURCE if (dom, T) in TRAFFIC else None,
                        "bytes_per_launch": dbytes, "avg_us": round(kern_us, 3)}
     return res
+
+
+STAGE_NAMES = ("router", "route_sort", "gate_up", "quant_act", "down", "combine")
+EMPTY_STAGE_US = 0.5  # an event pair around no launch measures well below this
 
 
 OPS_PER_TOKEN = (K + 1) * 3 * 2 * E * FF   # int8 ops of the routed pairs and the shared row: 56,623,104
@@ -215,7 +222,23 @@ def bench_config(eng, layer, copies, T, steps, warmup, torch):
         # Q4_K gate/up (144 B per 256) and Q6_K down (210 B per 256): 2,039,808 B per expert
         ebytes = 2 * FF * (E // 256 * 144) + E * (FF // 256 * 210)
         res["mfma"] = mfma_block(T, ms, (NE + 1) * ebytes + ROUTER_BYTES + 2 * T * E * 4)
+        # the dominant kernel, the exact Q4_K gate/up, alone over the copies:
+        # its algorithmic bytes are every expert's gate and up rows, the Q8 of
+        # h with its scales and block sums, and the f32 intermediate written
+        kern_us = 1e3 * eng.time_stage(moes, h_dev.data_ptr(), T, out_dev.data_ptr(), "gate_up", steps)
+        gbytes = (NE + 1) * 2 * FF * (E // 256 * 144) + T * E * 5 // 4 + (T * K + T) * FF * 4
+        ach = gbytes / (kern_us * 1e-6)
+        res["roofline"] = {"kernel": "gate_up (exact Q4_K, k_gu_exact)", "bound": "hbm",
+                           "achieved": round(ach / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                           "frac": round(ach / HBM_PEAK, 4), "bytes_per_launch": gbytes, "avg_us": round(kern_us, 3),
+                           "traffic": KQ_TRAFFIC.get("gate_up"), "traffic_source": KQ_TRAFFIC_SOURCE}
     return res
+
+
+# as TRAFFIC, for the Q4_K/Q6_K layer at T = 2048 and the BF16 layer at T = 4096
+KQ_TRAFFIC_SOURCE = "profiles/prefill_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated)"
+KQ_TRAFFIC = {"gate_up": 688458752, "down": 585138176}
+BF_TRAFFIC = {"gate_up": 1470939136, "down": 931569664}
 
 
 def bench_bf16_stack(eng, T, n_layers, passes, torch):
@@ -251,6 +274,12 @@ def bench_bf16_stack(eng, T, n_layers, passes, torch):
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / (passes * n_layers)
+    # the dominant kernel, the BF16 grouped gate/up, alone over the layers
+    # (on x, the last pass's output, ~N(0,1) rows): weights of every expert,
+    # h's bf16 halves read, the intermediate's halves written
+    kern_us = 1e3 * eng.time_stage(moes, x.data_ptr(), T, x0.data_ptr(), "gate_up", n_layers)
+    gbytes = (NE + 1) * 2 * FF * E * 2 + T * E * 4 + (T * K + T) * FF * 4
+    kach = gbytes / (kern_us * 1e-6)
     P = T * K
     flops = 2.0 * (P + T) * 3 * E * FF  # routed pairs and shared rows, gate + up + down
     U = NE  # every expert is routed at this T
@@ -268,6 +297,11 @@ def bench_bf16_stack(eng, T, n_layers, passes, torch):
                          "frac": round(layer_bytes / (ms * 1e-3) / HBM_PEAK, 4)},
             "mfma": {"achieved": round(flops / (ms * 1e-3) / 1e12, 1), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(flops / (ms * 1e-3) / 2.5e15, 4)},
+            "kernel_roofline": {"kernel": "gate_up (BF16 grouped GEMM, k_mfma_bf16)", "bound": "hbm",
+                                "achieved": round(kach / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                                "frac": round(kach / HBM_PEAK, 4), "bytes_per_launch": gbytes,
+                                "avg_us": round(kern_us, 3), "traffic": BF_TRAFFIC.get("gate_up"),
+                                "traffic_source": KQ_TRAFFIC_SOURCE},
             "hbm_GBps": round(layer_bytes / (ms * 1e-3) / 1e9, 1)}
 
 

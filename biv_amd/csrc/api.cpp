@@ -6,6 +6,7 @@
 #include "layout.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <new>
 #include <cstdlib>
 #include <cstdarg>
@@ -456,6 +457,32 @@ int scratch_fit(biv_hip_ctx *ctx, const biv_hip_moe *m, int T)
 constexpr size_t NOALLOC_BYTES = (size_t)48 << 20;
 static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
 
+// The context that holds each GPU's copy of `scratch`: the first to call the
+// no-allocation entry point on that device, until it is destroyed.  Another
+// context calling it on the same device gets BIV_HIP_E_BUSY rather than a
+// silent race over the same bytes.
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::atomic<biv_hip_ctx *> g_noalloc_owner[NOALLOC_MAX_DEVICES];
+
+int noalloc_claim(biv_hip_ctx *ctx)
+{
+    if (ctx->device >= NOALLOC_MAX_DEVICES)
+        return fail(ctx, BIV_HIP_E_INVALID, "no-allocation scratch: device %d past %d", ctx->device,
+                    NOALLOC_MAX_DEVICES);
+    biv_hip_ctx *owner = nullptr;
+    if (g_noalloc_owner[ctx->device].compare_exchange_strong(owner, ctx) || owner == ctx) return 0;
+    return fail(ctx, BIV_HIP_E_BUSY, "the no-allocation scratch of device %d is held by another context",
+                ctx->device);
+}
+
+void noalloc_release(biv_hip_ctx *ctx)
+{
+    if (ctx->device < NOALLOC_MAX_DEVICES) {
+        biv_hip_ctx *mine = ctx;
+        g_noalloc_owner[ctx->device].compare_exchange_strong(mine, nullptr);
+    }
+}
+
 // Carve the buffers of a forward of T tokens of layer m out of the context's
 // copy of `scratch` (256-byte aligned pieces).  No allocation.
 int noalloc_scratch(biv_hip_ctx *ctx, const biv_hip_moe *m, int T, Scratch &s);
@@ -792,6 +819,7 @@ void biv_hip_destroy(biv_hip_ctx *ctx)
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    noalloc_release(ctx);
     scratch_free(ctx);
     for (auto &v : ctx->ev_fwd)
         for (auto e : v) (void)hipEventDestroy(e);
@@ -938,6 +966,9 @@ int biv_hip_moe_forward_device_noalloc(biv_hip_ctx *ctx, const biv_hip_moe *moe,
     int rc = check_fwd(ctx, moe, h_dev, n, out_dev);
     if (rc) return rc;
     if (n == 0) return 0;
+    // stage timing would create events (an allocation)
+    if (ctx->timing) return fail(ctx, BIV_HIP_E_INVALID, "the no-allocation entry point runs with timing off");
+    if ((rc = noalloc_claim(ctx))) return rc;
     HIP_TRY(ctx, hipSetDevice(ctx->device), "hipSetDevice");
     Scratch s;
     if ((rc = noalloc_scratch(ctx, moe, n, s))) return rc;

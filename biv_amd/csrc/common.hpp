@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "bf16_split.h"
+
 namespace biv {
 
 enum : int { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4K = 12, T_Q6K = 14, T_BF16 = 30 };
@@ -89,13 +91,6 @@ struct RouterArgs {
 // matrix-core router)
 int prep_min_t();
 
-// bf16 bits of x, round to nearest, ties to even (finite x); NaN stays NaN
-__device__ inline uint32_t bf16_bits(float x)
-{
-    const uint32_t u = __float_as_uint(x);
-    if (x != x) return 0x7FC0u;
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
 // router logits + gate_inp logit + Q8 quantisation of h
 hipError_t launch_router(const RouterArgs &a, hipStream_t st);
 // route every token, then sort the pairs into dispatch order (`work`:

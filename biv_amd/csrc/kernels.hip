@@ -784,8 +784,7 @@ template <int NS> __global__ __launch_bounds__(64 * PREP_TOK) void k_prep(Router
             for (int m = 0; m < 8; m++) {
                 const int e = 128 * g + 16 * m + c;
                 const float x = r[(e >> 5) * PREP_PITCH + (e & 31)];
-                hb[m] = bf16_bits(x);
-                lb[m] = bf16_bits(x - __uint_as_float(hb[m] << 16));
+                bf16_split(x, &hb[m], &lb[m]);
             }
             a.xh[(size_t)t * (E / 8) + ch] = make_uint4(hb[0] | hb[1] << 16, hb[2] | hb[3] << 16, hb[4] | hb[5] << 16,
                                                         hb[6] | hb[7] << 16);

@@ -74,8 +74,7 @@ __global__ __launch_bounds__(256) void k_split_bf16(const float *__restrict__ x,
 #pragma unroll
     for (int m = 0; m < 8; m++) {
         const float v = x[r * K + 128 * g + 16 * m + L];
-        h[m] = bf16_bits(v);
-        lo[m] = bf16_bits(v - __uint_as_float(h[m] << 16));
+        bf16_split(v, &h[m], &lo[m]);
     }
     xh[idx] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
     xl[idx] = make_uint4(lo[0] | lo[1] << 16, lo[2] | lo[3] << 16, lo[4] | lo[5] << 16, lo[6] | lo[7] << 16);
@@ -333,8 +332,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
             for (int m = 0; m < 8; m++) {
                 const float v = trow(p)[16 * m + L];
-                h[m] = bf16_bits(v);
-                lo[m] = bf16_bits(v - __uint_as_float(h[m] << 16));
+                bf16_split(v, &h[m], &lo[m]);
             }
             const size_t c = (size_t)(beg + p) * nc + 16 * rt + L;
             a.xo_h[c] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);

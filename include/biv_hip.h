@@ -51,6 +51,7 @@ enum {
     BIV_HIP_E_FORMAT = -5,  /* malformed GGUF (Error::Truncated, BadMagic, UnsupportedVersion, ...; error.rs:13-25) */
     BIV_HIP_E_IO = -6,      /* a GGUF file cannot be opened or mapped */
     BIV_HIP_E_MISSING = -7, /* GGUF key or tensor absent (Error::MissingKey / MissingTensor, error.rs:28-29) */
+    BIV_HIP_E_BUSY = -8,    /* the GPU's no-allocation scratch is held by another context (no counterpart) */
 };
 
 /* forward flags */
@@ -125,8 +126,12 @@ int biv_hip_moe_forward_device(biv_hip_ctx *ctx, const biv_hip_moe *moe, const f
  * It calls no allocator: its scratch is a fixed 48 MiB device buffer of the
  * library, one per GPU, held until the process ends, which fits up to about
  * 350 tokens of a qwen35moe layer (n_embd 2048, n_ff 512, 256 experts, k 8);
- * larger n gives BIV_HIP_E_INVALID.  Every call on a GPU uses the same
- * buffer: calls that overlap on one GPU (two streams, two contexts) race. */
+ * larger n gives BIV_HIP_E_INVALID.  The buffer is reserved in every
+ * process that loads the library and is not counted by
+ * biv_hip_device_bytes.  The first context to call this on a GPU holds that
+ * GPU's buffer until it is destroyed; another context gets BIV_HIP_E_BUSY.
+ * Calls of the holding context that overlap (two streams) race.  Stage
+ * timing (biv_hip_set_timing) must be off: it creates events. */
 int biv_hip_moe_forward_device_noalloc(biv_hip_ctx *ctx, const biv_hip_moe *moe, const float *h_dev, int n,
                                        float *out_dev, unsigned flags);
 

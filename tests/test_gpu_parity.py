@@ -178,6 +178,12 @@ def test_q8_full_layer_decode(orc, engine, T):
     rel, t = full_parity(orc, engine, layer, moe, h, block_dots=T <= 5)
     if T <= 5:
         check_act(orc, layer, h, t)
+    else:
+        # T = 40: the int32 block dots of the chain kernels on a seeded sample
+        # of the 360 rows (the oracle redoes each row's 3 matrices), the first
+        # and last routed pair and the first and last shared row included
+        P = T * layer.k
+        check_block_dots_sampled(orc, layer, h, t, n_pairs=96, seed=7, extra=(0, P - 1, P, P + T - 1))
 
 
 @pytest.mark.parametrize("skew", [0.13, 1.0])
@@ -188,16 +194,20 @@ def test_q8_prefill_zipf_512(orc, engine, skew):
     layer, moe = layer_for(engine, seed=1)
     h = synth.zipf_bias_tokens(layer, 3, 512, scale=skew)
     ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
-    got, t = moe.ffn_taps(h, dots=skew == 1.0)
+    got, t = moe.ffn_taps(h)
     assert np.array_equal(t["ids"], ids)
     check_dispatch(t, ids, 512, layer.k)
-    if skew == 1.0:
-        # the matrix-core kernels' int32 block dots (exact gate/up word dots,
-        # int8 MFMA down) on a sample of the 4608 rows, hot expert included
-        hot = int(np.bincount(ids.ravel()).argmax())
-        p_hot = np.flatnonzero(t["pair_expert"] == hot)
-        check_block_dots_sampled(orc, layer, h, t, n_pairs=160, seed=5,
-                                 extra=(int(p_hot[0]), int(p_hot[-1]), 512 * 8, 512 * 8 + 511))
+    # the matrix-core kernels' int32 block dots (exact gate/up word dots, int8
+    # MFMA down) on a sample of the 4608 rows, the hot expert's first and last
+    # pair, an expert's single pair (a one-pair slot) and the first and last
+    # shared row included
+    cnt = np.bincount(ids.ravel(), minlength=layer.n_expert)
+    hot = int(cnt.argmax())
+    p_hot = np.flatnonzero(t["pair_expert"] == hot)
+    extra = [int(p_hot[0]), int(p_hot[-1]), 512 * 8, 512 * 8 + 511]
+    if (cnt == 1).any():
+        extra.append(int(np.flatnonzero(t["pair_expert"] == int(np.flatnonzero(cnt == 1)[0]))[0]))
+    check_block_dots_sampled(orc, layer, h, t, n_pairs=160, seed=5 + int(skew * 10), extra=tuple(extra))
     check_output(ref, got, min_exact=0.0)  # int8 MFMA: f32 block sums in their own order
     again = moe.ffn(h)
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
