@@ -367,6 +367,39 @@ def test_bf16_stack_steps(orc, engine):
         engine.free(nd)
 
 
+def test_bf16_stack_depth_40(orc, engine):
+    """configs[4]'s depth: x += moe(rms_norm(x)) through 40 applications of a
+    256-expert BF16 layer (each with its own norm weights), a T = 64 chunk on
+    the matrix-core path, against the oracle after every layer: the error the
+    bf16 halves' own summation order leaves must not grow past the bar over
+    the stack (the chunk is smaller than the bench's T = 4096 so that the
+    oracle keeps up; the full chunk is checked for two layers above)."""
+    print("case bf16 stack depth 40", flush=True)
+    T, E, eps, L = 64, 2048, 1e-6, 40
+    layer = synth.make_layer(seed=300, types=(BF16, BF16, BF16))
+    moe = engine.moe(layer)
+    rng = np.random.default_rng(9)
+    norms = [(1.0 + 0.02 * rng.standard_normal(E)).astype(np.float32) for _ in range(L)]
+    x = synth.make_tokens(702, T, offsets=True)
+    xd, nd = engine.malloc(x.nbytes), engine.malloc(E * 4)
+    rels = []
+    try:
+        engine.h2d(xd, x)
+        ref = x.copy()
+        for w in norms:
+            engine.h2d(nd, w)
+            moe.ffn_step_device(xd, nd, eps, T)
+            got = engine.d2h(np.empty_like(x), xd)
+            ref = ref + orc.moe(layer, orc.rms_norm(ref, w, eps), threads=8)
+            rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+            rels.append(float(np.abs(ref.astype(np.float64) - got).max()) / rms)
+    finally:
+        engine.free(xd)
+        engine.free(nd)
+    print("max|d|/RMS of x by layer:", " ".join(f"{r:.1e}" for r in rels))
+    assert max(rels) <= TOL, rels
+
+
 def test_kquant_layer(orc, engine):
     """Q4_K gate/up, Q6_K down (config 4) at small expert count."""
     print("case kquant", flush=True)
