@@ -68,13 +68,37 @@ def build(verbose=False, defines=(), out=OUT):
 PROBES = os.path.join(ROOT, "tests", "probes")
 
 
+def link_flags(src_path):
+    """Libraries a probe names on a first line '// probe-links: biv_hip oracle':
+    the in-tree libbiv_hip.so and the CPU oracle (test checker), found at run
+    time relative to the executable."""
+    with open(src_path) as f:
+        first = f.readline()
+    if not first.startswith("// probe-links:"):
+        return []
+    libs = first.split(":", 1)[1].split()
+    flags = []
+    for lib in libs:
+        if lib == "biv_hip":
+            flags += ["-L", HERE, "-lbiv_hip", "-Wl,-rpath,$ORIGIN/../../biv_amd"]
+        elif lib == "oracle":
+            sys.path.insert(0, os.path.join(ROOT, "oracle"))
+            import oracle
+            oracle.build()
+            flags += ["-L", os.path.dirname(oracle.LIB_PATH), "-loracle", "-Wl,-rpath,$ORIGIN/../../oracle/_build"]
+        else:
+            raise RuntimeError(f"{src_path}: unknown probe library {lib}")
+    return flags
+
+
 def build_probes(verbose=False):
     """The GPU test programs under tests/probes (each <name>.cpp, HIP, into
     an executable <name> beside it)."""
     outs = []
     for src in sorted(f for f in os.listdir(PROBES) if f.endswith(".cpp")):
         exe = os.path.join(PROBES, src[:-4])
-        cmd = [hipcc()] + FLAGS + ["-x", "hip", os.path.join(PROBES, src), "-o", exe]
+        cmd = [hipcc()] + FLAGS + ["-x", "hip", os.path.join(PROBES, src), "-o", exe] + \
+            link_flags(os.path.join(PROBES, src))
         if verbose:
             print(" ".join(cmd))
         r = subprocess.run(cmd, capture_output=True, text=True)

@@ -66,3 +66,34 @@ def test_code_objects_are_gfx950():
     from biv_amd import hip
     data = open(hip.LIB_PATH, "rb").read()
     assert b"gfx950" in data
+
+
+def test_cpp_host_mirror_compiles_and_throws_without_gpu(tmp_path):
+    """include/biv_hip.hpp is standalone C++17 over the C ABI: g++ builds a
+    program against libbiv_hip.so, and constructing an Engine on a host with
+    no gfx950 device throws Error carrying BIV_HIP_E_DEVICE and the message
+    (Error::Backend at construction)."""
+    import subprocess
+    src = tmp_path / "m.cpp"
+    src.write_text(r'''
+#include "biv_hip.hpp"
+#include <cstdio>
+int main() {
+    try {
+        biv::hip::Engine e(0);
+        std::printf("constructed\n");
+        return 2;
+    } catch (const biv::hip::Error &err) {
+        std::printf("code=%d msg=%s\n", err.code(), err.what());
+        return err.code() == BIV_HIP_E_DEVICE ? 0 : 1;
+    }
+}
+''')
+    exe = tmp_path / "m"
+    lib = os.path.join(ROOT, "biv_amd")
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), str(src), "-o",
+                    str(exe), "-L", lib, "-lbiv_hip", f"-Wl,-rpath,{lib}"], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "code=-3" in r.stdout and "device" in r.stdout
