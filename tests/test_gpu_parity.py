@@ -141,20 +141,24 @@ def full_parity(orc, engine, layer, moe, h, block_dots=True, min_exact=0.9999):
     return rel, t
 
 
-@pytest.mark.parametrize("T", [1, 2, 5, 9, 64, 65, 100, 1100])
+@pytest.mark.parametrize("T", [1, 2, 5, 9, 16, 17, 63, 64, 65, 100, 255, 256, 512, 513, 1100])
 def test_q8_small_layer(orc, engine, T):
     """T <= 16 quantises the SwiGLU intermediate inside the down kernel,
     larger T in its own launch; below 64 every sum runs in the x86 order and
     the outputs carry the oracle's bits.  From T = 64 the experts run on the
-    int8 matrix cores (slots of 32 pairs): the int32 block dots are still the
+    int8 matrix cores (slots of 16 pairs): the int32 block dots are still the
     oracle's exactly (checked from the MFMA kernel's own taps), the f32 sums
-    over blocks run in another order, so the outputs meet the tolerance."""
+    over blocks run in another order, so the outputs meet the tolerance.
+    Each side of every switch: 16/17 (down + combine in one launch), 63/64
+    (chain kernels / matrix cores), 255/256 (decode router / pre-pass and
+    matrix-core router), 512/513 (the dispatch scan inside the placement /
+    its own launch)."""
     print(f"case q8 small T={T}", flush=True)
     layer, moe = layer_for(engine, seed=21, n_expert=32)
     h = synth.make_tokens(100 + T, T, offsets=True)
     # T = 1100: 69 blocks of 16 tokens, so the dispatch scan's runs are 5
     # blocks long and the last one is partial
-    full_parity(orc, engine, layer, moe, h, block_dots=T <= 9 or T in (64, 65),
+    full_parity(orc, engine, layer, moe, h, block_dots=T <= 17 or T in (64, 65),
                 min_exact=0.9999 if T < 64 else 0.0)
 
 
