@@ -273,7 +273,7 @@ def test_bf16_layer(orc, engine, T):
     full_parity(orc, engine, layer, moe, h, block_dots=False)
 
 
-@pytest.mark.parametrize("T,n_expert", [(64, 32), (300, 32), (512, 256)])
+@pytest.mark.parametrize("T,n_expert", [(64, 32), (255, 32), (256, 32), (300, 32), (512, 256)])
 def test_bf16_mfma(orc, engine, T, n_expert):
     """BF16 experts from T = 64 on the matrix cores: activations split into
     two bf16 halves, products exact, sums in the MFMA's order.  The bar is the
@@ -408,12 +408,12 @@ def test_kquant_layer(orc, engine):
     """Q4_K gate/up, Q6_K down (config 4) at small expert count."""
     print("case kquant", flush=True)
     layer, moe = layer_for(engine, seed=31, n_expert=32, types=(Q4K, Q4K, Q6K))
-    for T in (1, 6):
+    for T in (1, 6, 16, 17, 63):  # each side of the fused down + combine (16/17)
         h = synth.make_tokens(300 + T, T, offsets=True)
         full_parity(orc, engine, layer, moe, h)
 
 
-@pytest.mark.parametrize("T", [64, 100])
+@pytest.mark.parametrize("T", [64, 100, 255, 256])
 def test_kquant_prefill(orc, engine, T):
     """From T = 64 the K-quant experts run on the int8 matrix cores: Q4_K
     gate/up bit for bit (word dots from masked MFMAs, the x86 chains and the
