@@ -91,6 +91,7 @@ struct biv_hip_ctx {
     bool timing = false;
     // down and combine in one launch at decode sizes (BIV_HIP_FUSED_DC=0 turns it off)
     bool fused_dc = true;
+    bool gu_route = true; // T = 1: the routing inside the gate/up launch
     std::vector<hipEvent_t> ev_pool;
     std::vector<std::vector<hipEvent_t>> ev_fwd;
     // this GPU's copy of the no-allocation scratch (hipGetSymbolAddress)
@@ -619,10 +620,15 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
         if (h == s.h_stage) return fail(ctx, BIV_HIP_E_INVALID, "post_norm input aliases its output");
         h = s.h_stage; // every later use of h takes the normalised rows
     }
+    // One token (decode): every gate/up workgroup routes it from the logits
+    // (the same bits in each) and the first writes the dispatch records, so
+    // there is no route launch.  The taps take the separate launches.
+    const bool gu_route = ctx->gu_route && T == 1 && !mf_gu && !mq_gu && !dm.gate && !dm.up && !dm.down &&
+                          k <= 8 && k % 4 == 0 && ne >= k && ne <= 256 && u_max == k;
     MARK();
     if (run(0)) HIP_TRY(ctx, biv::launch_router(ra, st), "router");
     MARK();
-    if (run(1)) HIP_TRY(ctx, biv::launch_route_sort(s.logits, ne, k, T, chunk, s.dp, ctr_rs, st), "route and dispatch");
+    if (run(1) && !gu_route) HIP_TRY(ctx, biv::launch_route_sort(s.logits, ne, k, T, chunk, s.dp, ctr_rs, st), "route and dispatch");
     MARK();
 
     biv::MvArgs a{};
@@ -643,6 +649,11 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     a.T = T;
     a.P = P;
     a.u_max = u_max;
+    if (gu_route) {
+        a.logits = s.logits;
+        a.n_expert = ne;
+        a.k = k;
+    }
     if (run(2)) {
         if (mf_gu) {
             biv::MfArgs g{};
@@ -810,6 +821,8 @@ int biv_hip_create(int device, biv_hip_ctx **out)
     }
     const char *fdc = getenv("BIV_HIP_FUSED_DC");
     ctx->fused_dc = !(fdc && fdc[0] == '0');
+    const char *gur = getenv("BIV_HIP_GU_ROUTE");
+    ctx->gu_route = !(gur && gur[0] == '0');
     *out = ctx;
     return 0;
 }

@@ -119,6 +119,11 @@ struct MvArgs {
     int n_sh;               // grid slots of the shared expert, which come first (set by the launcher)
     int sh_chunk;           // tokens per shared-expert slot (set by the launcher)
     int n_rt;               // row tiles of a slot (matrix-core launches; set by the launcher)
+    // gate/up of one token with the routing inside (no route launch): the
+    // router's logits [n_expert]; every routed workgroup routes the token,
+    // the first writes the dispatch records
+    const float *logits;
+    int n_expert, k;
 };
 
 // gate/up: out[p][r] = silu(gate_r . x) * (up_r . x) for every pair and shared row.

@@ -806,7 +806,8 @@ __device__ inline void load_logits(const float *__restrict__ logits, int n_exper
     }
 }
 
-// v: the token's logits (load_logits); tab: the exp table in LDS
+// v: the token's logits (load_logits); tab: the exp table in LDS; ids / wts
+// (global, may be null) and lds_ids / lds_wts (may be null) take the routes
 __device__ void route_token(float (&v)[RPER], const uint64_t *tab, int n_expert, int k, int t, float *es,
                             int *__restrict__ ids, float *__restrict__ wts, int *lds_ids, float *lds_wts)
 {
@@ -978,8 +979,10 @@ __device__ void route_token(float (&v)[RPER], const uint64_t *tab, int n_expert,
     s = fmaxf(s, 1.0f / 16384.0f);
     if (lane < k) {
         const float w = sel_p / s;
-        ids[(size_t)t * k + lane] = sel_i;
-        wts[(size_t)t * k + lane] = w;
+        if (ids) {
+            ids[(size_t)t * k + lane] = sel_i;
+            wts[(size_t)t * k + lane] = w;
+        }
         if (lds_ids) {
             lds_ids[t * k + lane] = sel_i;
             lds_wts[t * k + lane] = w;
@@ -1996,9 +1999,10 @@ constexpr int XT = 8; // activation rows staged in LDS at a time
 // Each wave holds NSET sets of rows (four groups each), all loaded before the
 // first token: more bytes in flight per wave.
 // WPE: the waves per SIMD the register allocation must allow.
-template <int TY, int K, bool GATEUP, bool DUMP, int NSET, bool QX, int WPE>
+template <int TY, int K, bool GATEUP, bool DUMP, int NSET, bool QX, int WPE, bool ROUTE = false>
 __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(WPE, 8))) void k_chain_mv(MvArgs a)
 {
+    static_assert(!ROUTE || (GATEUP && !QX), "the routing runs inside gate/up only");
     constexpr int S = K / 64;
     constexpr int RPW = GATEUP ? 2 : 4; // rows per set of a wave
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -2011,6 +2015,12 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
         tok0 = u * a.sh_chunk; // the shared expert's tokens [tok0, tok0 + cnt)
         beg = a.P + tok0;
         cnt = min(a.sh_chunk, a.T - tok0);
+    } else if constexpr (ROUTE) {
+        // one token: routed slot j is the pair at dispatch position j, the
+        // token's j-th expert in ascending id (route_token below names it)
+        beg = u - a.n_sh;
+        cnt = 1;
+        sl.tok[0] = 0;
     } else {
         sl = a.dp.slots[u - a.n_sh];
         if (sl.cnt == 0) return; // uniform over the workgroup
@@ -2096,6 +2106,39 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
     // order, so a gather issued after the weight loads would start only once
     // the weights are in.
     issue_chunk(0, min(XC, cnt));
+    if constexpr (ROUTE) {
+        // The token's routing (route, model.rs:256-268) by wave 0 of every
+        // routed workgroup, the same bits in each: the logits and exp's table
+        // go out behind the activation row, then the k experts in rank order
+        // land in LDS and slot j takes the one with j experts below it.  The
+        // first routed workgroup also writes the routes and the dispatch
+        // records that down + combine read (sort_pairs_small, T = 1).
+        __shared__ uint64_t rtab[32];
+        __shared__ float res[MAX_EXPERTS];
+        __shared__ __align__(16) int rids[TOPK_FAST];
+        __shared__ int rmark[WAVE];
+        __shared__ float rwts[TOPK_FAST];
+        __shared__ int rexp;
+        if (!shared && wave == 0) {
+            const bool lead = blockIdx.x == 0 && u == a.n_sh;
+            float lg[RPER];
+            load_logits(a.logits, a.n_expert, 0, lg);
+            if (lane < 32) rtab[lane] = exp_tab_g[lane];
+            wave_lds_sync();
+            route_token(lg, rtab, a.n_expert, a.k, 0, res, lead ? a.dp.ids : nullptr, lead ? a.dp.wts : nullptr, rids,
+                        rwts);
+            wave_lds_sync();
+            if (lane < a.k) {
+                const int ei = rids[lane];
+                int below = 0;
+                for (int j = 0; j < a.k; j++) below += rids[j] < ei;
+                if (below == beg) rexp = ei;
+            }
+            if (lead) sort_pairs_small(rids, rwts, a.k, 1, a.dp, rmark);
+        }
+        __syncthreads();
+        if (!shared) e = rexp;
+    }
     Chain<TY, K> wc[NSET];
 #pragma unroll
     for (int q = 0; q < NSET; q++) {
@@ -2464,7 +2507,10 @@ hipError_t launch_case(const MvArgs &a, int rows, int slots, hipStream_t st)
         // occupancy asked of the register allocator (Q8_0 only: the K-quant
         // chains need more registers than 4 waves per SIMD leave)
         constexpr int WPE = TY != T_Q8_0 || DUMP ? 1 : KK >= 2048 && !QX ? 5 : 4;
-        k_chain_mv<TY, KK, GATEUP, DUMP, NSET, QX, WPE><<<grid, MV_WAVES * WAVE, 0, st>>>(a);
+        if (GATEUP && !DUMP && !QX && a.logits)
+            k_chain_mv<TY, KK, GATEUP, false, NSET, false, WPE, GATEUP && !DUMP && !QX>
+                <<<grid, MV_WAVES * WAVE, 0, st>>>(a);
+        else k_chain_mv<TY, KK, GATEUP, DUMP, NSET, QX, WPE><<<grid, MV_WAVES * WAVE, 0, st>>>(a);
         return hipGetLastError();
     }
 }
@@ -2512,6 +2558,11 @@ hipError_t launch_mv(const MvArgs &a, hipStream_t st)
                                : launch_mv_q<GATEUP, false>(a, routed, shared, st);
     };
     const bool has_shared = a.sa.q != nullptr;
+    // routing inside gate/up: one token, k <= 8 distinct experts in k slots
+    // (sort_pairs_small takes the pairs four at a time)
+    if (a.logits && (!GATEUP || a.T != 1 || a.k > TOPK_FAST || a.k % 4 || a.u_max != a.k || a.n_expert < a.k ||
+                     a.n_expert > MAX_EXPERTS))
+        return hipErrorInvalidValue;
     // routed and shared in one launch when they share types and shape
     const bool together = has_shared && a.sa.ty == a.a.ty && a.sa.cols == a.a.cols && a.sa.rows == a.a.rows &&
                           (!GATEUP || a.sb.ty == a.b.ty);

@@ -190,6 +190,45 @@ def test_q8_full_layer_decode(orc, engine, T):
         check_block_dots_sampled(orc, layer, h, t, n_pairs=96, seed=7, extra=(0, P - 1, P, P + T - 1))
 
 
+@pytest.mark.parametrize("case", ["full", "ties", "k4", "no_shared", "kquant", "bf16", "mixed_shared"])
+def test_decode_routing_in_gateup(orc, engine, case):
+    """One token routes inside the gate/up launch (no route launch; the taps
+    without block dots take that path): every routed workgroup routes the
+    token, the first writes the routes and dispatch records that down +
+    combine read.  Its logits, ids, weights, dispatch order and output
+    against the oracle, and the same bits as the path with the separate
+    route launch (the block-dot taps take it)."""
+    import dataclasses
+    print(f"case routing in gate/up {case}", flush=True)
+    kw = dict(full=dict(seed=1), ties=dict(seed=71, n_expert=32), k4=dict(seed=73, n_expert=32, k=4),
+              no_shared=dict(seed=75, n_expert=32, shared=False),
+              kquant=dict(seed=77, n_expert=32, types=(Q4K, Q4K, Q6K)),
+              bf16=dict(seed=79, n_expert=32, types=(BF16, BF16, BF16)),
+              mixed_shared=dict(seed=41, n_expert=16, types=(Q4K, Q4K, Q6K), shared_types=(Q8_0, Q8_0, Q8_0)))[case]
+    if case == "ties":
+        # router rows repeated: probabilities tie inside the top k and across the k-th place
+        layer = synth.make_layer(**kw)
+        W = layer.router.data.view(np.float32).reshape(32, -1).copy()
+        W[:] = W[np.arange(32) % 5]
+        layer = dataclasses.replace(layer, router=dataclasses.replace(layer.router, data=W.view(np.uint8).reshape(-1)))
+        moe = engine.moe(layer)
+    else:
+        layer, moe = layer_for(engine, **kw)
+    for seed in (500, 501, 502):
+        h = synth.make_tokens(seed, 1)
+        ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
+        got, t = moe.ffn_taps(h, dots=False)
+        if orc.detect_level() >= orc.AVX2:
+            assert np.array_equal(t["logits"].view(np.uint32), logits.view(np.uint32)), "router logits differ"
+        assert np.array_equal(t["ids"], ids), "top-k ids differ"
+        assert np.allclose(t["weights"], w, rtol=1e-5, atol=1e-7)
+        check_dispatch(t, ids, 1, layer.k)
+        check_output(ref, got)
+        tapped, t2 = moe.ffn_taps(h)
+        assert np.array_equal(t["weights"].view(np.uint32), t2["weights"].view(np.uint32))
+        assert np.array_equal(got.view(np.uint32), tapped.view(np.uint32)), "differs from the route-launch path"
+
+
 @pytest.mark.parametrize("skew", [0.13, 1.0])
 def test_q8_prefill_zipf_512(orc, engine, skew):
     """T=512 with Zipf-skewed routing (config 3): skew 0.13 puts ~60 tokens on
