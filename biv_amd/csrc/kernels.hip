@@ -636,50 +636,65 @@ __device__ inline void cas_desc(unsigned &a, unsigned &b)
     b = lo;
 }
 
-__device__ inline void topk_lists(const unsigned (&key)[MAX_EXPERTS_PER_LANE], unsigned (&lst)[TOPK_FAST])
+// The top TOPK_FAST of two descending lists, descending: the top half of a
+// bitonic merge (a against b reversed), then the half-cleaners that sort it.
+__device__ inline void merge_top(const unsigned (&a)[TOPK_FAST], const unsigned (&b)[TOPK_FAST], unsigned (&out)[TOPK_FAST])
 {
-    static_assert(MAX_EXPERTS_PER_LANE == 4 && TOPK_FAST == 8, "list shapes (and the four rows of route_token)");
-    unsigned a0 = key[0], a1 = key[1], a2 = key[2], a3 = key[3];
-    cas_desc(a0, a1);
-    cas_desc(a2, a3);
-    cas_desc(a0, a2);
-    cas_desc(a1, a3);
-    cas_desc(a1, a2);
-    lst[0] = a0;
-    lst[1] = a1;
-    lst[2] = a2;
-    lst[3] = a3;
+    unsigned m[TOPK_FAST];
 #pragma unroll
-    for (int i = 4; i < TOPK_FAST; i++) lst[i] = 0u;
+    for (int i = 0; i < TOPK_FAST; i++) m[i] = max(a[i], b[TOPK_FAST - 1 - i]);
+#pragma unroll
+    for (int d = TOPK_FAST / 2; d >= 1; d >>= 1)
+#pragma unroll
+        for (int i = 0; i < TOPK_FAST; i++)
+            if ((i & d) == 0) cas_desc(m[i], m[i + d]);
+#pragma unroll
+    for (int i = 0; i < TOPK_FAST; i++) out[i] = m[i];
+}
+
+// N keys per lane (N = 2 or 4)
+template <int N> __device__ inline void topk_lists(const unsigned (&key)[N], unsigned (&lst)[TOPK_FAST])
+{
+    static_assert((N == 2 || N == 4) && TOPK_FAST == 8, "list shapes");
+#pragma unroll
+    for (int i = 0; i < TOPK_FAST; i++) lst[i] = i < N ? key[i] : 0u;
+    if constexpr (N == 4) {
+        cas_desc(lst[0], lst[1]);
+        cas_desc(lst[2], lst[3]);
+        cas_desc(lst[0], lst[2]);
+        cas_desc(lst[1], lst[3]);
+        cas_desc(lst[1], lst[2]);
+    } else {
+        cas_desc(lst[0], lst[1]);
+    }
     // six levels; each lane meets a partner holding a list of other keys:
     // within a row of 16 lanes by DPP (quad_perm [1,0,3,2], [2,3,0,1], then
     // row_ror 4 and 8: after the second level a lane group of four is
-    // uniform, and rotating by one group, then by two, meets disjoint groups),
-    // then lanes 16 and 32 apart
+    // uniform, and rotating by one group, then by two, meets disjoint
+    // groups); then rows 16 lanes apart and halves 32 apart, swapped between
+    // two copies of each entry (v_permlane16_swap / v_permlane32_swap): each
+    // lane then holds both lists of its pair of rows (halves), one in each
+    // copy, and merges them (the merge is symmetric)
 #pragma unroll
     for (int lvl = 0; lvl < 6; lvl++) {
-        unsigned m[TOPK_FAST];
+        unsigned A[TOPK_FAST], B[TOPK_FAST];
 #pragma unroll
         for (int i = 0; i < TOPK_FAST; i++) {
-            const int v = (int)lst[TOPK_FAST - 1 - i];
-            m[i] = (unsigned)(lvl == 0   ? __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false)
-                              : lvl == 1 ? __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false)
-                              : lvl == 2 ? __builtin_amdgcn_mov_dpp(v, 0x124, 0xF, 0xF, false)
-                              : lvl == 3 ? __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false)
-                              : lvl == 4 ? __shfl_xor(v, 16)
-                                         : __shfl_xor(v, 32));
+            if (lvl < 4) {
+                A[i] = lst[i];
+                const int v = (int)lst[i];
+                B[i] = (unsigned)(lvl == 0   ? __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false)
+                                  : lvl == 1 ? __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false)
+                                  : lvl == 2 ? __builtin_amdgcn_mov_dpp(v, 0x124, 0xF, 0xF, false)
+                                             : __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false));
+            } else {
+                const auto r = lvl == 4 ? __builtin_amdgcn_permlane16_swap(lst[i], lst[i], false, false)
+                                        : __builtin_amdgcn_permlane32_swap(lst[i], lst[i], false, false);
+                A[i] = r[0];
+                B[i] = r[1];
+            }
         }
-        // the top half of a bitonic merge of two descending lists, then the
-        // half-cleaners that sort that bitonic sequence
-#pragma unroll
-        for (int i = 0; i < TOPK_FAST; i++) m[i] = max(lst[i], m[i]);
-#pragma unroll
-        for (int d = TOPK_FAST / 2; d >= 1; d >>= 1)
-#pragma unroll
-            for (int i = 0; i < TOPK_FAST; i++)
-                if ((i & d) == 0) cas_desc(m[i], m[i + d]);
-#pragma unroll
-        for (int i = 0; i < TOPK_FAST; i++) lst[i] = m[i];
+        merge_top(A, B, lst);
     }
 }
 
@@ -806,6 +821,9 @@ __device__ inline void load_logits(const float *__restrict__ logits, int n_exper
     }
 }
 
+__device__ void route_select(unsigned (&key)[RPER], const unsigned (&lst)[TOPK_FAST], int n_expert, int k, int t,
+                             float *es, int *__restrict__ ids, float *__restrict__ wts, int *lds_ids, float *lds_wts);
+
 // v: the token's logits (load_logits); tab: the exp table in LDS; ids / wts
 // (global, may be null) and lds_ids / lds_wts (may be null) take the routes
 __device__ void route_token(float (&v)[RPER], const uint64_t *tab, int n_expert, int k, int t, float *es,
@@ -850,16 +868,88 @@ __device__ void route_token(float (&v)[RPER], const uint64_t *tab, int n_expert,
     unsigned key[RPER];
 #pragma unroll
     for (int j = 0; j < RPER; j++) key[j] = lane + WAVE * j < n_expert ? __float_as_uint(v[j] * inv) + 1u : 0u;
+    // The k largest keys as a sorted list in every lane: each lane sorts its
+    // own, then six butterfly levels merge a lane's list with its partner's,
+    // keeping the top TOPK_FAST (bitonic merge).
+    unsigned lst[TOPK_FAST];
+    if (k <= TOPK_FAST) topk_lists<RPER>(key, lst);
+    route_select(key, lst, n_expert, k, t, es, ids, wts, lds_ids, lds_wts);
+}
+
+// The set of one token's k routed experts without the softmax's sum, when
+// the exps alone decide it: with e = exp(x - max) (e <= 1, sum <= 256, so
+// inv = 1 / sum lies in [1/256, 1]), the probabilities p = e * inv round
+// monotonically, and two exps at least 16 ulps apart, both at least 2^-100
+// (the smaller may be +0 instead), give distinct p.  So when the k-th
+// largest exp stands that far above the next one, the k largest p are the
+// k largest exps, whatever the sum.  Returns false (decide by route_token)
+// for NaN or infinite logits, a narrower gap, or equal exps at the k-th
+// place.  On success *e_out is the u-th smallest expert id of the set (the
+// expert of dispatch slot u for one token).  v: the token's logits
+// (load_logits), unchanged; tab: this wave's exp table in LDS; k <= 8.
+__device__ bool route_set_by_exps(const float (&v)[RPER], const uint64_t *tab, int n_expert, int k, int u, int *e_out)
+{
+    const int lane = threadIdx.x & 63;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < RPER; j++) mx = fmaxf(mx, v[j]);
+    if (mx != mx) mx = -INFINITY;
+    mx = ordered_to_f32(wave_max_u32(f32_to_ordered(mx)));
+    unsigned ek[RPER], lst[TOPK_FAST];
+#pragma unroll
+    for (int j = 0; j < RPER; j++) {
+        const float ev = exp_lds(v[j] - mx, tab);
+        ek[j] = lane + WAVE * j < n_expert ? __float_as_uint(ev) + 1u : 0u;
+    }
+    topk_lists<RPER>(ek, lst);
+    unsigned kth = lst[0];
+#pragma unroll
+    for (int r = 1; r < TOPK_FAST; r++) kth = r == k - 1 ? lst[r] : kth;
+    unsigned long long m[RPER];
+    unsigned below = 0u;
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < RPER; j++) {
+        m[j] = __ballot(ek[j] >= kth);
+        cnt += __popcll(m[j]);
+        below = max(below, ek[j] < kth ? ek[j] : 0u);
+    }
+    const unsigned next = wave_max_u32(below);
+    constexpr unsigned ONE = 0x3F800000u + 1u, TINY = 0x0D800000u + 1u; // keys of 1.0 and 2^-100
+    const bool ok = lst[0] <= ONE && cnt == k && kth >= TINY &&
+                    (next <= 1u || (next >= TINY && kth - next >= 16u));
+    if (!ok) return false;
+    int need = u, id = 0;
+    bool found = false;
+#pragma unroll
+    for (int j = 0; j < RPER; j++) {
+        unsigned long long mm = m[j];
+        const int c = __popcll(mm);
+        if (!found && need < c) {
+            for (int q = 0; q < need; q++) mm &= mm - 1ull;
+            id = WAVE * j + __ffsll((long long)mm) - 1;
+            found = true;
+        } else if (!found) {
+            need -= c;
+        }
+    }
+    *e_out = id;
+    return true;
+}
+
+// The selection from the probabilities: key[j] = bits(p) + 1 of expert
+// lane + 64 j (0 past n_expert) and, for k <= TOPK_FAST, lst, the top
+// TOPK_FAST keys in descending order (equal keys as separate entries).  The
+// expert of rank r: the keys equal to the r-th, in index order, skipping
+// those equal keys already ranked (lower index first); weights p / max(sum
+// of the k in rank order, 1/16384).  es: this wave's LDS scratch.
+__device__ void route_select(unsigned (&key)[RPER], const unsigned (&lst)[TOPK_FAST], int n_expert, int k, int t,
+                             float *es, int *__restrict__ ids, float *__restrict__ wts, int *lds_ids, float *lds_wts)
+{
+    const int lane = threadIdx.x & 63;
     float sel_p = 0.0f, s = 0.0f;
     int sel_i = 0;
     if (k <= TOPK_FAST) {
-        // The k largest keys as a sorted list in every lane: each lane sorts
-        // its own, then six butterfly levels merge a lane's list with its
-        // partner's, keeping the top TOPK_FAST (bitonic merge).  Then the
-        // expert of rank r: the keys equal to the r-th, in index order,
-        // skipping those equal keys already ranked (lower index first).
-        unsigned lst[TOPK_FAST];
-        topk_lists(key, lst);
         // Every lane holds the same list.  Without equal keys among the k
         // largest (nor between the k-th and the next), exactly k keys are at
         // least the k-th, and each one's rank is the number of listed keys
@@ -1999,6 +2089,27 @@ constexpr int XT = 8; // activation rows staged in LDS at a time
 // Each wave holds NSET sets of rows (four groups each), all loaded before the
 // first token: more bytes in flight per wave.
 // WPE: the waves per SIMD the register allocation must allow.
+// The routing workgroup of a one-token gate/up launch: the token's routes
+// (route_token) to dp.ids / dp.wts and the dispatch records that down +
+// combine read (sort_pairs_small), by its first wave.
+__device__ inline void route_t1_records(const MvArgs &a)
+{
+    __shared__ uint64_t tab[32];
+    __shared__ float es[MAX_EXPERTS];
+    __shared__ __align__(16) int ids[TOPK_FAST];
+    __shared__ float wts[TOPK_FAST];
+    __shared__ int mark[WAVE];
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x >= WAVE) return;
+    float lg[RPER];
+    load_logits(a.logits, a.n_expert, 0, lg);
+    if (lane < 32) tab[lane] = exp_tab_g[lane];
+    wave_lds_sync();
+    route_token(lg, tab, a.n_expert, a.k, 0, es, a.dp.ids, a.dp.wts, ids, wts);
+    wave_lds_sync();
+    sort_pairs_small(ids, wts, a.k, 1, a.dp, mark);
+}
+
 template <int TY, int K, bool GATEUP, bool DUMP, int NSET, bool QX, int WPE, bool ROUTE = false>
 __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(WPE, 8))) void k_chain_mv(MvArgs a)
 {
@@ -2017,7 +2128,12 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
         cnt = min(a.sh_chunk, a.T - tok0);
     } else if constexpr (ROUTE) {
         // one token: routed slot j is the pair at dispatch position j, the
-        // token's j-th expert in ascending id (route_token below names it)
+        // token's j-th expert in ascending id (named below); the row of
+        // workgroups past the slots is the routing workgroup's
+        if (u >= a.n_sh + a.u_max) {
+            if (blockIdx.x == 0) route_t1_records(a);
+            return; // uniform over the workgroup
+        }
         beg = u - a.n_sh;
         cnt = 1;
         sl.tok[0] = 0;
@@ -2107,37 +2223,41 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
     // the weights are in.
     issue_chunk(0, min(XC, cnt));
     if constexpr (ROUTE) {
-        // The token's routing (route, model.rs:256-268) by wave 0 of every
-        // routed workgroup, the same bits in each: the logits and exp's table
-        // go out behind the activation row, then the k experts in rank order
-        // land in LDS and slot j takes the one with j experts below it.  The
-        // first routed workgroup also writes the routes and the dispatch
-        // records that down + combine read (sort_pairs_small, T = 1).
+        // The token's expert for this slot (route, model.rs:256-268), the
+        // same in every routed workgroup: from the exps alone when they
+        // decide the set (route_set_by_exps), else by the whole routing
+        // (route_token), whose k experts in rank order land in LDS; slot j
+        // takes the one with j experts below it.  The logits and exp's
+        // table go out behind the activation row.  The routing workgroup
+        // (route_t1_records) writes the routes and dispatch records.
         __shared__ uint64_t rtab[32];
         __shared__ float res[MAX_EXPERTS];
-        __shared__ __align__(16) int rids[TOPK_FAST];
-        __shared__ int rmark[WAVE];
+        __shared__ int rids[TOPK_FAST];
         __shared__ float rwts[TOPK_FAST];
         __shared__ int rexp;
-        if (!shared && wave == 0) {
-            const bool lead = blockIdx.x == 0 && u == a.n_sh;
-            float lg[RPER];
-            load_logits(a.logits, a.n_expert, 0, lg);
-            if (lane < 32) rtab[lane] = exp_tab_g[lane];
-            wave_lds_sync();
-            route_token(lg, rtab, a.n_expert, a.k, 0, res, lead ? a.dp.ids : nullptr, lead ? a.dp.wts : nullptr, rids,
-                        rwts);
-            wave_lds_sync();
-            if (lane < a.k) {
-                const int ei = rids[lane];
-                int below = 0;
-                for (int j = 0; j < a.k; j++) below += rids[j] < ei;
-                if (below == beg) rexp = ei;
+        if (!shared) { // uniform over the workgroup
+            if (wave == 0) {
+                float lg[RPER];
+                load_logits(a.logits, a.n_expert, 0, lg);
+                if (lane < 32) rtab[lane] = exp_tab_g[lane];
+                wave_lds_sync();
+                int ex;
+                if (route_set_by_exps(lg, rtab, a.n_expert, a.k, beg, &ex)) {
+                    if (lane == 0) rexp = ex;
+                } else {
+                    route_token(lg, rtab, a.n_expert, a.k, 0, res, nullptr, nullptr, rids, rwts);
+                    wave_lds_sync();
+                    if (lane < a.k) {
+                        const int ei = rids[lane];
+                        int nb = 0;
+                        for (int j = 0; j < a.k; j++) nb += rids[j] < ei;
+                        if (nb == beg) rexp = ei;
+                    }
+                }
             }
-            if (lead) sort_pairs_small(rids, rwts, a.k, 1, a.dp, rmark);
+            __syncthreads();
+            e = rexp;
         }
-        __syncthreads();
-        if (!shared) e = rexp;
     }
     Chain<TY, K> wc[NSET];
 #pragma unroll
@@ -2509,7 +2629,7 @@ hipError_t launch_case(const MvArgs &a, int rows, int slots, hipStream_t st)
         constexpr int WPE = TY != T_Q8_0 || DUMP ? 1 : KK >= 2048 && !QX ? 5 : 4;
         if (GATEUP && !DUMP && !QX && a.logits)
             k_chain_mv<TY, KK, GATEUP, false, NSET, false, WPE, GATEUP && !DUMP && !QX>
-                <<<grid, MV_WAVES * WAVE, 0, st>>>(a);
+                <<<dim3(grid.x, grid.y + 1), MV_WAVES * WAVE, 0, st>>>(a); // + the routing workgroup's row
         else k_chain_mv<TY, KK, GATEUP, DUMP, NSET, QX, WPE><<<grid, MV_WAVES * WAVE, 0, st>>>(a);
         return hipGetLastError();
     }
@@ -2520,7 +2640,10 @@ template <bool GATEUP, bool DUMP, bool QX>
 hipError_t launch_mv_t(MvArgs a, int routed, int shared, hipStream_t st)
 {
     const DevMat &M = routed ? a.a : a.sa;
-    if (!routed) a.u_max = 0;
+    if (!routed) {
+        a.u_max = 0;
+        a.logits = nullptr; // the routed launch routes
+    }
     a.sh_chunk = XT;
     a.n_sh = shared ? (a.T + XT - 1) / XT : 0;
     const int slots = a.u_max + a.n_sh;
