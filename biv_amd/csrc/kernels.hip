@@ -884,10 +884,11 @@ __device__ void route_token(float (&v)[RPER], const uint64_t *tab, int n_expert,
 // largest exp stands that far above the next one, the k largest p are the
 // k largest exps, whatever the sum.  Returns false (decide by route_token)
 // for NaN or infinite logits, a narrower gap, or equal exps at the k-th
-// place.  On success *e_out is the u-th smallest expert id of the set (the
-// expert of dispatch slot u for one token).  v: the token's logits
-// (load_logits), unchanged; tab: this wave's exp table in LDS; k <= 8.
-__device__ bool route_set_by_exps(const float (&v)[RPER], const uint64_t *tab, int n_expert, int k, int u, int *e_out)
+// place; on success m[j] bit l is set for expert l + 64 j of the set.
+// v: the token's logits (load_logits), unchanged; tab: this wave's exp
+// table in LDS; k <= 8.
+__device__ bool route_set_masks(const float (&v)[RPER], const uint64_t *tab, int n_expert, int k,
+                                unsigned long long (&m)[RPER])
 {
     const int lane = threadIdx.x & 63;
     float mx = -INFINITY;
@@ -905,7 +906,6 @@ __device__ bool route_set_by_exps(const float (&v)[RPER], const uint64_t *tab, i
     unsigned kth = lst[0];
 #pragma unroll
     for (int r = 1; r < TOPK_FAST; r++) kth = r == k - 1 ? lst[r] : kth;
-    unsigned long long m[RPER];
     unsigned below = 0u;
     int cnt = 0;
 #pragma unroll
@@ -916,25 +916,7 @@ __device__ bool route_set_by_exps(const float (&v)[RPER], const uint64_t *tab, i
     }
     const unsigned next = wave_max_u32(below);
     constexpr unsigned ONE = 0x3F800000u + 1u, TINY = 0x0D800000u + 1u; // keys of 1.0 and 2^-100
-    const bool ok = lst[0] <= ONE && cnt == k && kth >= TINY &&
-                    (next <= 1u || (next >= TINY && kth - next >= 16u));
-    if (!ok) return false;
-    int need = u, id = 0;
-    bool found = false;
-#pragma unroll
-    for (int j = 0; j < RPER; j++) {
-        unsigned long long mm = m[j];
-        const int c = __popcll(mm);
-        if (!found && need < c) {
-            for (int q = 0; q < need; q++) mm &= mm - 1ull;
-            id = WAVE * j + __ffsll((long long)mm) - 1;
-            found = true;
-        } else if (!found) {
-            need -= c;
-        }
-    }
-    *e_out = id;
-    return true;
+    return lst[0] <= ONE && cnt == k && kth >= TINY && (next <= 1u || (next >= TINY && kth - next >= 16u));
 }
 
 // The selection from the probabilities: key[j] = bits(p) + 1 of expert
@@ -2089,25 +2071,34 @@ constexpr int XT = 8; // activation rows staged in LDS at a time
 // Each wave holds NSET sets of rows (four groups each), all loaded before the
 // first token: more bytes in flight per wave.
 // WPE: the waves per SIMD the register allocation must allow.
-// The routing workgroup of a one-token gate/up launch: the token's routes
-// (route_token) to dp.ids / dp.wts and the dispatch records that down +
-// combine read (sort_pairs_small), by its first wave.
-__device__ inline void route_t1_records(const MvArgs &a)
+// The routing workgroup of a small-batch gate/up launch (T <= XT, slots of
+// 64 pairs): the tokens' routes (route_token, a wave per token in turn) to
+// dp.ids / dp.wts and the dispatch records that down + combine read
+// (sort_pairs_small or sort_pairs_wave, as k_route_sort), in LDS scratch of
+// ROUTE_SCRATCH bytes.
+constexpr int ROUTE_SCRATCH = 1024 + 4 * 1024 + 512 + 2048 + 2048;
+__device__ inline void route_records(const MvArgs &a, void *scratch)
 {
-    __shared__ uint64_t tab[32];
-    __shared__ float es[MAX_EXPERTS];
-    __shared__ __align__(16) int ids[TOPK_FAST];
-    __shared__ float wts[TOPK_FAST];
-    __shared__ int mark[WAVE];
-    const int lane = threadIdx.x & 63;
-    if (threadIdx.x >= WAVE) return;
-    float lg[RPER];
-    load_logits(a.logits, a.n_expert, 0, lg);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    char *sc = static_cast<char *>(scratch);
+    uint64_t *tab = reinterpret_cast<uint64_t *>(sc) + 32 * wave;
+    float *es = reinterpret_cast<float *>(sc + 1024) + MAX_EXPERTS * wave;
+    int *ids = reinterpret_cast<int *>(sc + 1024 + 4 * 1024);
+    float *wts = reinterpret_cast<float *>(ids + 64);
+    int *cnt = reinterpret_cast<int *>(wts + 64), *first = cnt + 2 * MAX_EXPERTS, *sfirst = first + MAX_EXPERTS;
     if (lane < 32) tab[lane] = exp_tab_g[lane];
     wave_lds_sync();
-    route_token(lg, tab, a.n_expert, a.k, 0, es, a.dp.ids, a.dp.wts, ids, wts);
-    wave_lds_sync();
-    sort_pairs_small(ids, wts, a.k, 1, a.dp, mark);
+    for (int t = wave; t < a.T; t += MV_WAVES) {
+        float lg[RPER];
+        load_logits(a.logits, a.n_expert, t, lg);
+        route_token(lg, tab, a.n_expert, a.k, t, es, a.dp.ids, a.dp.wts, ids, wts);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int P = a.T * a.k;
+        if (P <= BIV_SMALL_SORT_P && P % 4 == 0) sort_pairs_small(ids, wts, a.k, a.T, a.dp, cnt);
+        else sort_pairs_wave(ids, wts, a.n_expert, a.k, a.T, 64, a.dp, cnt, first, sfirst);
+    }
 }
 
 template <int TY, int K, bool GATEUP, bool DUMP, int NSET, bool QX, int WPE, bool ROUTE = false>
@@ -2127,16 +2118,13 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
         beg = a.P + tok0;
         cnt = min(a.sh_chunk, a.T - tok0);
     } else if constexpr (ROUTE) {
-        // one token: routed slot j is the pair at dispatch position j, the
-        // token's j-th expert in ascending id (named below); the row of
-        // workgroups past the slots is the routing workgroup's
-        if (u >= a.n_sh + a.u_max) {
-            if (blockIdx.x == 0) route_t1_records(a);
-            return; // uniform over the workgroup
-        }
-        beg = u - a.n_sh;
-        cnt = 1;
-        sl.tok[0] = 0;
+        // the slot's expert, first position and tokens come from the
+        // routing below; meanwhile every token's row is staged (row t =
+        // token t)
+        beg = 0;
+        cnt = a.T;
+#pragma unroll
+        for (int j = 0; j < SLOT_TOKS; j++) sl.tok[j] = j;
     } else {
         sl = a.dp.slots[u - a.n_sh];
         if (sl.cnt == 0) return; // uniform over the workgroup
@@ -2171,7 +2159,10 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
     constexpr int ROW16 = K / 16 + K / 128;
     constexpr int NTH = MV_WAVES * WAVE;
     constexpr int NPC = F32IN ? XC * K / 4 / NTH : (XC * ROW16 + NTH - 1) / NTH; // pieces per thread
-    __shared__ int4 stage[BF ? 1 : (XC * ROW16 + NTH - 1) / NTH * NTH];
+    constexpr int STAGE16 = BF ? 1 : (XC * ROW16 + NTH - 1) / NTH * NTH;
+    constexpr int RS16 = ROUTE ? ROUTE_SCRATCH / 16 : 1;
+    __shared__ int4 stage[STAGE16 > RS16 ? STAGE16 : RS16]; // also the routing workgroup's scratch
+    __shared__ int s_tok[XT];                                 // ROUTE: the slot's tokens (staged rows)
     __shared__ int4 fstage[F32IN ? NPC * NTH : 1];
     auto lds_load = [&](const void *src, int4 *dst_wave) {
         __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst_wave, 16, 0, 0);
@@ -2221,42 +2212,109 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
     // The first chunk's loads go out before the weights': loads complete in
     // order, so a gather issued after the weight loads would start only once
     // the weights are in.
+    if constexpr (ROUTE) {
+        // the row of workgroups past the slots: the routing workgroup's
+        if (u >= a.n_sh + a.u_max) {
+            if (blockIdx.x == 0) route_records(a, stage);
+            return; // uniform over the workgroup
+        }
+    }
     issue_chunk(0, min(XC, cnt));
     if constexpr (ROUTE) {
-        // The token's expert for this slot (route, model.rs:256-268), the
-        // same in every routed workgroup: from the exps alone when they
-        // decide the set (route_set_by_exps), else by the whole routing
-        // (route_token), whose k experts in rank order land in LDS; slot j
-        // takes the one with j experts below it.  The logits and exp's
-        // table go out behind the activation row.  The routing workgroup
-        // (route_t1_records) writes the routes and dispatch records.
-        __shared__ uint64_t rtab[32];
+        // The slot's record (route, model.rs:256-268, and the dispatch
+        // order of model.rs:866-873), the same in every routed workgroup:
+        // each token's expert set from its exps when they decide it
+        // (route_set_masks, a wave per token in turn), else from its whole
+        // routing (route_token, by wave 0); then slot us is the us-th expert
+        // of their union in ascending id, its pairs follow those of the
+        // lower experts, its tokens ascend (every expert holds at most T <=
+        // 32 pairs: one slot each).  The logits and exp's table go out
+        // behind the activation rows.  The routing workgroup
+        // (route_records) writes the routes and dispatch records.
+        __shared__ uint64_t rtab[MV_WAVES][32];
         __shared__ float res[MAX_EXPERTS];
         __shared__ int rids[TOPK_FAST];
         __shared__ float rwts[TOPK_FAST];
-        __shared__ int rexp;
+        __shared__ unsigned long long rmask[XT][RPER];
+        __shared__ int rok[XT], rhdr[3];
         if (!shared) { // uniform over the workgroup
-            if (wave == 0) {
+            if (lane < 32) rtab[wave][lane] = exp_tab_g[lane];
+            wave_lds_sync();
+            for (int t = wave; t < a.T; t += MV_WAVES) {
                 float lg[RPER];
-                load_logits(a.logits, a.n_expert, 0, lg);
-                if (lane < 32) rtab[lane] = exp_tab_g[lane];
-                wave_lds_sync();
-                int ex;
-                if (route_set_by_exps(lg, rtab, a.n_expert, a.k, beg, &ex)) {
-                    if (lane == 0) rexp = ex;
-                } else {
-                    route_token(lg, rtab, a.n_expert, a.k, 0, res, nullptr, nullptr, rids, rwts);
+                load_logits(a.logits, a.n_expert, t, lg);
+                unsigned long long mk[RPER];
+                const bool ok = route_set_masks(lg, rtab[wave], a.n_expert, a.k, mk);
+                if (lane < RPER) {
+                    unsigned long long mine = mk[0];
+#pragma unroll
+                    for (int j = 1; j < RPER; j++) mine = lane == j ? mk[j] : mine;
+                    rmask[t][lane] = mine;
+                }
+                if (lane == 0) rok[t] = ok;
+            }
+            __syncthreads();
+            if (wave == 0) {
+                for (int t = 0; t < a.T; t++) {
+                    if (rok[t]) continue; // uniform
+                    float lg[RPER];
+                    load_logits(a.logits, a.n_expert, t, lg);
+                    route_token(lg, rtab[0], a.n_expert, a.k, 0, res, nullptr, nullptr, rids, rwts);
                     wave_lds_sync();
-                    if (lane < a.k) {
-                        const int ei = rids[lane];
-                        int nb = 0;
-                        for (int j = 0; j < a.k; j++) nb += rids[j] < ei;
-                        if (nb == beg) rexp = ei;
+#pragma unroll
+                    for (int j = 0; j < RPER; j++) {
+                        bool in = false;
+                        for (int q = 0; q < a.k; q++) in |= rids[q] == lane + WAVE * j;
+                        const unsigned long long mj = __ballot(in);
+                        if (lane == 0) rmask[t][j] = mj;
                     }
+                    wave_lds_sync();
+                }
+                unsigned long long un[RPER];
+#pragma unroll
+                for (int j = 0; j < RPER; j++) {
+                    un[j] = 0ull;
+                    for (int t = 0; t < a.T; t++) un[j] |= rmask[t][j];
+                }
+                int need = u - a.n_sh, ex = -1;
+#pragma unroll
+                for (int j = 0; j < RPER; j++) {
+                    const int c = __popcll(un[j]);
+                    if (ex < 0 && need < c) {
+                        unsigned long long mm = un[j];
+                        for (int q = 0; q < need; q++) mm &= mm - 1ull;
+                        ex = WAVE * j + __ffsll((long long)mm) - 1;
+                    } else if (ex < 0) {
+                        need -= c;
+                    }
+                }
+                int bg = 0, nc = 0;
+                if (ex >= 0) {
+                    const int jw = ex >> 6;
+                    const unsigned long long lo = (1ull << (ex & 63)) - 1ull;
+                    for (int t = 0; t < a.T; t++) {
+#pragma unroll
+                        for (int j = 0; j < RPER; j++) {
+                            const unsigned long long mm = rmask[t][j];
+                            bg += __popcll(j < jw ? mm : j == jw ? mm & lo : 0ull);
+                        }
+                        if ((rmask[t][jw] >> (ex & 63)) & 1ull) {
+                            if (lane == 0) s_tok[nc] = t;
+                            nc++;
+                        }
+                    }
+                }
+                if (lane == 0) {
+                    rhdr[0] = ex;
+                    rhdr[1] = bg;
+                    rhdr[2] = nc;
                 }
             }
             __syncthreads();
-            e = rexp;
+            e = __builtin_amdgcn_readfirstlane(rhdr[0]);
+            if (e < 0) return; // an unused slot, uniform
+            beg = __builtin_amdgcn_readfirstlane(rhdr[1]);
+            cnt = __builtin_amdgcn_readfirstlane(rhdr[2]);
         }
     }
     Chain<TY, K> wc[NSET];
@@ -2308,18 +2366,20 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
         } else {
         for (int j = 0; j < nt; j++) {
             const int i = i0 + j;
-            const size_t xrow = GATEUP ? (size_t)(shared ? tok0 + i : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
+            // ROUTE: the pair's staged row is its token's
+            const int sj = ROUTE && !shared ? s_tok[j] : j;
+            const size_t xrow = GATEUP ? (size_t)(shared ? tok0 + i : ROUTE ? sj : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
             const size_t orow = (size_t)(beg + i);
             int xw[S];
             float xd[S];
 #pragma unroll
             for (int q = 0; q < S / 4; q++) {
-                const int4 v = stage[j * ROW16 + q * 16 + pi * 8 + l];
+                const int4 v = stage[sj * ROW16 + q * 16 + pi * 8 + l];
                 xw[4 * q] = v.x;
                 xw[4 * q + 1] = v.y;
                 xw[4 * q + 2] = v.z;
                 xw[4 * q + 3] = v.w;
-                const float4 f = *reinterpret_cast<const float4 *>(&stage[j * ROW16 + K / 16 + pi * (S / 4) + q]);
+                const float4 f = *reinterpret_cast<const float4 *>(&stage[sj * ROW16 + K / 16 + pi * (S / 4) + q]);
                 xd[4 * q] = f.x;
                 xd[4 * q + 1] = f.y;
                 xd[4 * q + 2] = f.z;
@@ -2683,8 +2743,10 @@ hipError_t launch_mv(const MvArgs &a, hipStream_t st)
     const bool has_shared = a.sa.q != nullptr;
     // routing inside gate/up: one token, k <= 8 distinct experts in k slots
     // (sort_pairs_small takes the pairs four at a time)
-    if (a.logits && (!GATEUP || a.T != 1 || a.k > TOPK_FAST || a.k % 4 || a.u_max != a.k || a.n_expert < a.k ||
-                     a.n_expert > MAX_EXPERTS))
+    // routing inside gate/up: up to XT tokens (all staged at once; f32-input
+    // BF16 rows for one token only), k <= 8, one slot per used expert
+    if (a.logits && (!GATEUP || a.T > XT || (a.T > 1 && a.a.ty == T_BF16) || a.k > TOPK_FAST ||
+                     a.n_expert < a.k || a.n_expert > MAX_EXPERTS || a.u_max != max_slots(a.n_expert, a.P, 64)))
         return hipErrorInvalidValue;
     // routed and shared in one launch when they share types and shape
     const bool together = has_shared && a.sa.ty == a.a.ty && a.sa.cols == a.a.cols && a.sa.rows == a.a.rows &&

@@ -190,16 +190,21 @@ def test_q8_full_layer_decode(orc, engine, T):
         check_block_dots_sampled(orc, layer, h, t, n_pairs=96, seed=7, extra=(0, P - 1, P, P + T - 1))
 
 
+@pytest.mark.parametrize("T", [1, 2, 3, 5])
 @pytest.mark.parametrize("case", ["full", "ties", "k4", "no_shared", "kquant", "bf16", "mixed_shared"])
-def test_decode_routing_in_gateup(orc, engine, case):
-    """One token routes inside the gate/up launch (no route launch; the taps
-    without block dots take that path): every routed workgroup routes the
-    token, the first writes the routes and dispatch records that down +
-    combine read.  Its logits, ids, weights, dispatch order and output
-    against the oracle, and the same bits as the path with the separate
-    route launch (the block-dot taps take it)."""
+def test_decode_routing_in_gateup(orc, engine, case, T):
+    """Up to 3 tokens route inside the gate/up launch (no route launch; the
+    taps without block dots take that path): every routed workgroup derives
+    its slot from the logits (the tokens' expert sets from their exps, or
+    their whole routing when the exps do not decide), and a routing
+    workgroup writes the routes and dispatch records that down + combine
+    read.  Its logits, ids, weights, dispatch order and output against the
+    oracle, and the same bits as the path with the separate route launch
+    (the block-dot taps take it).  BF16 gate/up routes inside for one token
+    only; its other T values, and T = 5, check the separate launch the same
+    way."""
     import dataclasses
-    print(f"case routing in gate/up {case}", flush=True)
+    print(f"case routing in gate/up {case} T={T}", flush=True)
     kw = dict(full=dict(seed=1), ties=dict(seed=71, n_expert=32), k4=dict(seed=73, n_expert=32, k=4),
               no_shared=dict(seed=75, n_expert=32, shared=False),
               kquant=dict(seed=77, n_expert=32, types=(Q4K, Q4K, Q6K)),
@@ -215,14 +220,14 @@ def test_decode_routing_in_gateup(orc, engine, case):
     else:
         layer, moe = layer_for(engine, **kw)
     for seed in (500, 501, 502):
-        h = synth.make_tokens(seed, 1)
+        h = synth.make_tokens(seed + 10 * T, T, offsets=T > 1)
         ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
         got, t = moe.ffn_taps(h, dots=False)
         if orc.detect_level() >= orc.AVX2:
             assert np.array_equal(t["logits"].view(np.uint32), logits.view(np.uint32)), "router logits differ"
         assert np.array_equal(t["ids"], ids), "top-k ids differ"
         assert np.allclose(t["weights"], w, rtol=1e-5, atol=1e-7)
-        check_dispatch(t, ids, 1, layer.k)
+        check_dispatch(t, ids, T, layer.k)
         check_output(ref, got)
         tapped, t2 = moe.ffn_taps(h)
         assert np.array_equal(t["weights"].view(np.uint32), t2["weights"].view(np.uint32))
