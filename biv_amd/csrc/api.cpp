@@ -92,7 +92,7 @@ struct biv_hip_ctx {
     // down and combine in one launch at decode sizes (BIV_HIP_FUSED_DC=0 turns it off)
     bool fused_dc = true;
     bool gu_route = true; // small batches: the routing inside the gate/up launch
-    int gu_route_t = 3;   // up to this many tokens (BIV_HIP_GU_ROUTE_T, at most 8)
+    int gu_route_t = 3;   // up to this many tokens (BIV_HIP_GU_ROUTE_T, at most 4)
     std::vector<hipEvent_t> ev_pool;
     std::vector<std::vector<hipEvent_t>> ev_fwd;
     // this GPU's copy of the no-allocation scratch (hipGetSymbolAddress)
@@ -628,8 +628,9 @@ int forward(biv_hip_ctx *ctx, const biv_hip_moe *m, const float *h, int T, float
     // its weight loads, which past 3 tokens costs more than the launch
     // (measured: T = 1, 2, 3 20.5 / 26.8 / 34.4 against 21.0 / 29.9 / 35.1 us
     // per Q8_0 layer with the route launch; T = 4, 5, 8 42.6 / 55 / 78
-    // against 40.3 / 45.7 / 58).  BF16 gate/up, which stages f32 rows, for one
-    // token.  The taps take the separate launches.
+    // against 40.3 / 45.7 / 58).  At most 4 (a wave per token).  BF16
+    // gate/up, which stages f32 rows, for one token.  The taps take the
+    // separate launches.
     const bool bf_gu = m->gate->m.ty == biv::T_BF16;
     const bool gu_route = ctx->gu_route && T <= ctx->gu_route_t && (T == 1 || !bf_gu) && !mf_gu && !mq_gu &&
                           !dm.gate && !dm.up && !dm.down && k <= 8 && ne >= k && ne <= 256 && chunk == 64;
@@ -831,7 +832,7 @@ int biv_hip_create(int device, biv_hip_ctx **out)
     ctx->fused_dc = !(fdc && fdc[0] == '0');
     const char *gur = getenv("BIV_HIP_GU_ROUTE");
     ctx->gu_route = !(gur && gur[0] == '0');
-    if (const char *gt = getenv("BIV_HIP_GU_ROUTE_T")) ctx->gu_route_t = std::max(1, std::min(8, atoi(gt)));
+    if (const char *gt = getenv("BIV_HIP_GU_ROUTE_T")) ctx->gu_route_t = std::max(1, std::min(4, atoi(gt)));
     *out = ctx;
     return 0;
 }

@@ -2077,6 +2077,7 @@ constexpr int XT = 8; // activation rows staged in LDS at a time
 // (sort_pairs_small or sort_pairs_wave, as k_route_sort), in LDS scratch of
 // ROUTE_SCRATCH bytes.
 constexpr int ROUTE_SCRATCH = 1024 + 4 * 1024 + 512 + 2048 + 2048;
+constexpr int GU_ROUTE_TMAX = 4; // tokens of the routing inside gate/up: a wave each
 __device__ inline void route_records(const MvArgs &a, void *scratch)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -2162,7 +2163,7 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
     constexpr int STAGE16 = BF ? 1 : (XC * ROW16 + NTH - 1) / NTH * NTH;
     constexpr int RS16 = ROUTE ? ROUTE_SCRATCH / 16 : 1;
     __shared__ int4 stage[STAGE16 > RS16 ? STAGE16 : RS16]; // also the routing workgroup's scratch
-    __shared__ int s_tok[XT];                                 // ROUTE: the slot's tokens (staged rows)
+    __shared__ int s_tok[MV_WAVES][GU_ROUTE_TMAX]; // ROUTE: the slot's tokens (staged rows), a copy per wave
     __shared__ int4 fstage[F32IN ? NPC * NTH : 1];
     auto lds_load = [&](const void *src, int4 *dst_wave) {
         __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst_wave, 16, 0, 0);
@@ -2235,46 +2236,62 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
         __shared__ float res[MAX_EXPERTS];
         __shared__ int rids[TOPK_FAST];
         __shared__ float rwts[TOPK_FAST];
-        __shared__ unsigned long long rmask[XT][RPER];
-        __shared__ int rok[XT], rhdr[3];
+        __shared__ unsigned long long rmask[GU_ROUTE_TMAX][RPER];
+        __shared__ int rok[GU_ROUTE_TMAX];
         if (!shared) { // uniform over the workgroup
-            if (lane < 32) rtab[wave][lane] = exp_tab_g[lane];
+            // a wave per token: exp's table, then its logits go out, then the
+            // table's store to LDS (which waits only for the loads before it)
+            const uint64_t tv = lane < 32 ? exp_tab_g[lane] : 0ull;
+            float lg[RPER];
+            if (wave < a.T) load_logits(a.logits, a.n_expert, wave, lg);
+            if (lane < 32) rtab[wave][lane] = tv;
             wave_lds_sync();
-            for (int t = wave; t < a.T; t += MV_WAVES) {
-                float lg[RPER];
-                load_logits(a.logits, a.n_expert, t, lg);
+            if (wave < a.T) {
                 unsigned long long mk[RPER];
                 const bool ok = route_set_masks(lg, rtab[wave], a.n_expert, a.k, mk);
                 if (lane < RPER) {
                     unsigned long long mine = mk[0];
 #pragma unroll
                     for (int j = 1; j < RPER; j++) mine = lane == j ? mk[j] : mine;
-                    rmask[t][lane] = mine;
+                    rmask[wave][lane] = mine;
                 }
-                if (lane == 0) rok[t] = ok;
+                if (lane == 0) rok[wave] = ok;
             }
-            __syncthreads();
-            if (wave == 0) {
-                for (int t = 0; t < a.T; t++) {
-                    if (rok[t]) continue; // uniform
-                    float lg[RPER];
-                    load_logits(a.logits, a.n_expert, t, lg);
-                    route_token(lg, rtab[0], a.n_expert, a.k, 0, res, nullptr, nullptr, rids, rwts);
-                    wave_lds_sync();
+            {
+                __syncthreads();
+                bool all_ok = true;
+                for (int t = 0; t < a.T; t++) all_ok &= __builtin_amdgcn_readfirstlane(rok[t]) != 0;
+                if (!all_ok) { // uniform, rare: the whole routing of the undecided tokens, by wave 0
+                    if (wave == 0) {
+                        for (int t = 0; t < a.T; t++) {
+                            if (rok[t]) continue; // uniform
+                            float lt[RPER];
+                            load_logits(a.logits, a.n_expert, t, lt);
+                            route_token(lt, rtab[0], a.n_expert, a.k, 0, res, nullptr, nullptr, rids, rwts);
+                            wave_lds_sync();
 #pragma unroll
-                    for (int j = 0; j < RPER; j++) {
-                        bool in = false;
-                        for (int q = 0; q < a.k; q++) in |= rids[q] == lane + WAVE * j;
-                        const unsigned long long mj = __ballot(in);
-                        if (lane == 0) rmask[t][j] = mj;
+                            for (int j = 0; j < RPER; j++) {
+                                bool in = false;
+                                for (int q = 0; q < a.k; q++) in |= rids[q] == lane + WAVE * j;
+                                const unsigned long long mj = __ballot(in);
+                                if (lane == 0) rmask[t][j] = mj;
+                            }
+                            wave_lds_sync();
+                        }
                     }
-                    wave_lds_sync();
+                    __syncthreads();
                 }
+                // every wave: the slot from the masks (us-th expert of the
+                // union; its pairs after those of the lower experts; its tokens)
+                // (uniform values in vector registers: the scalar registers
+                // are short here; e, beg and cnt move to them at the end)
+                auto mask_at = [&](int t, int j) { return rmask[t][j]; };
                 unsigned long long un[RPER];
 #pragma unroll
-                for (int j = 0; j < RPER; j++) {
-                    un[j] = 0ull;
-                    for (int t = 0; t < a.T; t++) un[j] |= rmask[t][j];
+                for (int j = 0; j < RPER; j++) un[j] = 0ull;
+                for (int t = 0; t < a.T; t++) {
+#pragma unroll
+                    for (int j = 0; j < RPER; j++) un[j] |= mask_at(t, j);
                 }
                 int need = u - a.n_sh, ex = -1;
 #pragma unroll
@@ -2288,33 +2305,30 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
                         need -= c;
                     }
                 }
-                int bg = 0, nc = 0;
-                if (ex >= 0) {
-                    const int jw = ex >> 6;
-                    const unsigned long long lo = (1ull << (ex & 63)) - 1ull;
-                    for (int t = 0; t < a.T; t++) {
+                if (__builtin_amdgcn_readfirstlane(ex) < 0) return; // an unused slot, uniform
+                const int jw = ex >> 6;
+                const unsigned long long lo = (1ull << (ex & 63)) - 1ull;
+                int bg = 0;
+                unsigned tm = 0u;
+                for (int t = 0; t < a.T; t++) {
 #pragma unroll
-                        for (int j = 0; j < RPER; j++) {
-                            const unsigned long long mm = rmask[t][j];
-                            bg += __popcll(j < jw ? mm : j == jw ? mm & lo : 0ull);
-                        }
-                        if ((rmask[t][jw] >> (ex & 63)) & 1ull) {
-                            if (lane == 0) s_tok[nc] = t;
-                            nc++;
-                        }
+                    for (int j = 0; j < RPER; j++) {
+                        if (j > jw) break;
+                        const unsigned long long mm = mask_at(t, j);
+                        bg += __popcll(j < jw ? mm : mm & lo);
+                        if (j == jw) tm |= (unsigned)((mm >> (ex & 63)) & 1ull) << t;
                     }
                 }
-                if (lane == 0) {
-                    rhdr[0] = ex;
-                    rhdr[1] = bg;
-                    rhdr[2] = nc;
+                e = __builtin_amdgcn_readfirstlane(ex);
+                beg = __builtin_amdgcn_readfirstlane(bg);
+                cnt = __builtin_amdgcn_readfirstlane(__popc(tm));
+                if (lane < GU_ROUTE_TMAX) {
+                    unsigned r = tm;
+                    for (int q = 0; q < lane; q++) r &= r - 1u;
+                    s_tok[wave][lane] = r ? __ffs(r) - 1 : 0;
                 }
+                wave_lds_sync();
             }
-            __syncthreads();
-            e = __builtin_amdgcn_readfirstlane(rhdr[0]);
-            if (e < 0) return; // an unused slot, uniform
-            beg = __builtin_amdgcn_readfirstlane(rhdr[1]);
-            cnt = __builtin_amdgcn_readfirstlane(rhdr[2]);
         }
     }
     Chain<TY, K> wc[NSET];
@@ -2367,19 +2381,20 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
         for (int j = 0; j < nt; j++) {
             const int i = i0 + j;
             // ROUTE: the pair's staged row is its token's
-            const int sj = ROUTE && !shared ? s_tok[j] : j;
+            const int sj = ROUTE && !shared ? s_tok[wave][j] : j;
             const size_t xrow = GATEUP ? (size_t)(shared ? tok0 + i : ROUTE ? sj : a.dp.pair_tok[beg + i]) : (size_t)(beg + i);
             const size_t orow = (size_t)(beg + i);
             int xw[S];
             float xd[S];
+            const int4 *srow = stage + sj * ROW16;
 #pragma unroll
             for (int q = 0; q < S / 4; q++) {
-                const int4 v = stage[sj * ROW16 + q * 16 + pi * 8 + l];
+                const int4 v = srow[q * 16 + pi * 8 + l];
                 xw[4 * q] = v.x;
                 xw[4 * q + 1] = v.y;
                 xw[4 * q + 2] = v.z;
                 xw[4 * q + 3] = v.w;
-                const float4 f = *reinterpret_cast<const float4 *>(&stage[sj * ROW16 + K / 16 + pi * (S / 4) + q]);
+                const float4 f = *reinterpret_cast<const float4 *>(&srow[K / 16 + pi * (S / 4) + q]);
                 xd[4 * q] = f.x;
                 xd[4 * q + 1] = f.y;
                 xd[4 * q + 2] = f.z;
@@ -2743,9 +2758,10 @@ hipError_t launch_mv(const MvArgs &a, hipStream_t st)
     const bool has_shared = a.sa.q != nullptr;
     // routing inside gate/up: one token, k <= 8 distinct experts in k slots
     // (sort_pairs_small takes the pairs four at a time)
-    // routing inside gate/up: up to XT tokens (all staged at once; f32-input
-    // BF16 rows for one token only), k <= 8, one slot per used expert
-    if (a.logits && (!GATEUP || a.T > XT || (a.T > 1 && a.a.ty == T_BF16) || a.k > TOPK_FAST ||
+    // routing inside gate/up: up to GU_ROUTE_TMAX tokens (a wave each, all
+    // staged at once; f32-input BF16 rows for one token only), k <= 8, one
+    // slot per used expert
+    if (a.logits && (!GATEUP || a.T > GU_ROUTE_TMAX || (a.T > 1 && a.a.ty == T_BF16) || a.k > TOPK_FAST ||
                      a.n_expert < a.k || a.n_expert > MAX_EXPERTS || a.u_max != max_slots(a.n_expert, a.P, 64)))
         return hipErrorInvalidValue;
     // routed and shared in one launch when they share types and shape
