@@ -41,8 +41,10 @@ def test_noalloc_matches_forward_device():
         layer = synth.make_layer(1)
         moe = eng.moe(layer)
         E = layer.n_embd
-        # T = 256: the prefill pre-pass and the matrix-core router
-        _match(eng, moe, E, ((256, False), (40, False), (5, False), (1, True)))
+        # T = 256: the prefill pre-pass and the matrix-core router; T <= 3:
+        # the routing inside the gate/up launch (its routing workgroup
+        # writes the dispatch records into the fixed scratch)
+        _match(eng, moe, E, ((256, False), (40, False), (5, False), (3, False), (2, True), (1, True)))
         big = 1000
         hd = eng.malloc(big * E * 4)
         try:
