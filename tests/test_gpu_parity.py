@@ -234,6 +234,42 @@ def test_decode_routing_in_gateup(orc, engine, case, T):
         assert np.array_equal(got.view(np.uint32), tapped.view(np.uint32)), "differs from the route-launch path"
 
 
+def _random_decode_configs(n):
+    rng = np.random.default_rng(2027)
+    out = []
+    for i in range(n):
+        ne = int(rng.choice([8, 16, 40, 64, 100, 256]))
+        k = int(rng.choice([kk for kk in (1, 2, 3, 4, 6, 8) if kk <= ne]))
+        kq = bool(rng.integers(2))
+        out.append(dict(seed=600 + i, n_expert=ne, k=k, n_embd=int(rng.choice([512, 1024])),
+                        shared=bool(rng.integers(2)), types=(Q4K, Q4K, Q6K) if kq else (Q8_0, Q8_0, Q8_0),
+                        T=int(rng.integers(1, 4))))
+    return out
+
+
+@pytest.mark.parametrize("cfg", _random_decode_configs(12), ids=lambda c: f"ne{c['n_expert']}-k{c['k']}-E{c['n_embd']}-T{c['T']}")
+def test_decode_routing_random_layers(orc, engine, cfg):
+    """Seeded random layer shapes through the routing inside gate/up (1 to 3
+    tokens: expert counts 8 to 256, k 1 to 8, with and without the shared
+    expert, Q8_0 and Q4_K/Q6_K): routes, dispatch and output against the
+    oracle, and the same bits as the route-launch path."""
+    cfg = dict(cfg)
+    T = cfg.pop("T")
+    print(f"case random decode {cfg} T={T}", flush=True)
+    layer = synth.make_layer(n_ff=512, n_ff_sh=512, **cfg)
+    moe = engine.moe(layer)
+    h = synth.make_tokens(cfg["seed"] + 1, T, n_embd=cfg["n_embd"], offsets=T > 1)
+    ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
+    got, t = moe.ffn_taps(h, dots=False)
+    assert np.array_equal(t["ids"], ids), "top-k ids differ"
+    assert np.allclose(t["weights"], w, rtol=1e-5, atol=1e-7)
+    check_dispatch(t, ids, T, layer.k)
+    check_output(ref, got)
+    tapped, t2 = moe.ffn_taps(h)
+    assert np.array_equal(t["weights"].view(np.uint32), t2["weights"].view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), tapped.view(np.uint32)), "differs from the route-launch path"
+
+
 @pytest.mark.parametrize("skew", [0.13, 1.0])
 def test_q8_prefill_zipf_512(orc, engine, skew):
     """T=512 with Zipf-skewed routing (config 3): skew 0.13 puts ~60 tokens on
