@@ -270,6 +270,47 @@ def test_decode_routing_random_layers(orc, engine, cfg):
     assert np.array_equal(got.view(np.uint32), tapped.view(np.uint32)), "differs from the route-launch path"
 
 
+def _random_prefill_configs(n):
+    rng = np.random.default_rng(2028)
+    kinds = [(Q8_0, Q8_0, Q8_0), (Q4K, Q4K, Q6K), (BF16, BF16, BF16), (Q4K, Q4K, Q8_0)]
+    out = []
+    for i in range(n):
+        ne = int(rng.choice([16, 40, 64, 128]))
+        k = int(rng.choice([1, 2, 4, 6, 8]))
+        out.append(dict(seed=700 + i, n_expert=ne, k=k, n_embd=int(rng.choice([512, 1024, 2048])),
+                        n_ff=int(rng.choice([512, 1024])), shared=bool(rng.integers(2)),
+                        types=kinds[i % len(kinds)], T=int(rng.integers(64, 701))))
+    return out
+
+
+@pytest.mark.parametrize("cfg", _random_prefill_configs(8),
+                         ids=lambda c: f"ty{c['types'][0]}-ne{c['n_expert']}-k{c['k']}-E{c['n_embd']}-F{c['n_ff']}-T{c['T']}")
+def test_prefill_random_layers(orc, engine, cfg):
+    """Seeded random layer shapes at prefill sizes (64 to 700 tokens, the
+    matrix-core kernels): Q8_0, Q4_K/Q6_K, BF16 and Q4_K gate/up with a Q8_0
+    down; expert counts 16 to 128, k 1 to 8, widths 512 to 2048, n_ff 512
+    or 1024, with and without the shared expert.  Ids, weights and dispatch
+    against the oracle, a sample of the int32 block dots (quantised types),
+    the output within the tolerance, bit-identical run to run."""
+    cfg = dict(cfg)
+    T = cfg.pop("T")
+    print(f"case random prefill {cfg} T={T}", flush=True)
+    layer = synth.make_layer(n_ff_sh=cfg["n_ff"], **cfg)
+    moe = engine.moe(layer)
+    h = synth.make_tokens(cfg["seed"] + 1, T, n_embd=cfg["n_embd"], offsets=True)
+    ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
+    dots = cfg["types"][0] != BF16
+    got, t = moe.ffn_taps(h, dots=dots)
+    assert np.array_equal(t["ids"], ids), "top-k ids differ"
+    assert np.allclose(t["weights"], w, rtol=1e-5, atol=1e-7)
+    check_dispatch(t, ids, T, layer.k)
+    if dots:
+        check_block_dots_sampled(orc, layer, h, t, n_pairs=24, seed=cfg["seed"])
+    check_output(ref, got, min_exact=0.0)
+    again = moe.ffn(h)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "not bit-identical run to run"
+
+
 @pytest.mark.parametrize("skew", [0.13, 1.0])
 def test_q8_prefill_zipf_512(orc, engine, skew):
     """T=512 with Zipf-skewed routing (config 3): skew 0.13 puts ~60 tokens on
