@@ -311,6 +311,33 @@ def test_prefill_random_layers(orc, engine, cfg):
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "not bit-identical run to run"
 
 
+@pytest.mark.parametrize("T", [1, 2, 5, 40, 64])
+def test_non_finite_tokens(orc, engine, T):
+    """A token whose hidden state holds a NaN, and one holding +Inf, among
+    finite ones: every router logit of the NaN token is NaN and the Inf
+    token's are +-Inf, so the softmax gives NaN probabilities, which
+    total_cmp ranks as equals (the ids in index order, model.rs:263) and the
+    outputs of those tokens are NaN.  Logits, ids and the NaN positions as
+    the oracle's; the finite tokens' results as with no such neighbour."""
+    print(f"case non-finite tokens T={T}", flush=True)
+    layer, moe = layer_for(engine, seed=81, n_expert=32)
+    h = synth.make_tokens(900 + T, T, offsets=T > 1)
+    h[0, 7] = np.nan
+    if T > 1:
+        h[T - 1, 100] = np.inf
+    ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
+    got, t = moe.ffn_taps(h, dots=False)
+    if orc.detect_level() >= orc.AVX2:
+        assert np.array_equal(t["logits"].view(np.uint32), logits.view(np.uint32)), "router logits differ"
+    assert np.array_equal(t["ids"], ids), "top-k ids differ"
+    assert np.array_equal(np.isnan(t["weights"]), np.isnan(w))
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "NaN positions differ"
+    bad = [0] + ([T - 1] if T > 1 else [])
+    ok = np.setdiff1d(np.arange(T), bad)
+    if ok.size:
+        check_output(ref[ok], got[ok], min_exact=0.9999 if T < 64 else 0.0)
+
+
 @pytest.mark.parametrize("skew", [0.13, 1.0])
 def test_q8_prefill_zipf_512(orc, engine, skew):
     """T=512 with Zipf-skewed routing (config 3): skew 0.13 puts ~60 tokens on
