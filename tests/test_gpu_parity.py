@@ -340,6 +340,27 @@ def test_non_finite_tokens(orc, engine, T, kind):
         check_output(ref[ok], got[ok], min_exact=0.9999 if T < 64 and kind != "bf16" else 0.0)
 
 
+@pytest.mark.parametrize("T,kind", [(16, "q8"), (40, "q8"), (300, "q8"), (1100, "q8"), (300, "kquant"),
+                                    (600, "bf16")])
+def test_every_token_same_experts(orc, engine, T, kind):
+    """Every token the same hidden state: all T tokens route to the same k
+    experts, each expert then holds T pairs (the most one expert can hold):
+    many full slots of one expert, its rows read by all of them, and the
+    dispatch's per-expert runs at their longest.  Against the oracle, and
+    every token's output identical to the first's."""
+    print(f"case same experts T={T} {kind}", flush=True)
+    types = dict(q8=(Q8_0, Q8_0, Q8_0), kquant=(Q4K, Q4K, Q6K), bf16=(BF16, BF16, BF16))[kind]
+    layer, moe = layer_for(engine, seed=83, n_expert=32, types=types)
+    h = np.repeat(synth.make_tokens(950, 1), T, axis=0)
+    ref, ids, w, logits = orc.moe(layer, h, threads=8, taps=True)
+    got, t = moe.ffn_taps(h, dots=False)
+    assert np.array_equal(t["ids"], ids), "top-k ids differ"
+    assert (ids == ids[0]).all()
+    check_dispatch(t, ids, T, layer.k)
+    check_output(ref, got, min_exact=0.9999 if T < 64 else 0.0)
+    assert np.array_equal(got.view(np.uint32), np.repeat(got[:1], T, axis=0).view(np.uint32)), "tokens differ"
+
+
 @pytest.mark.parametrize("skew", [0.13, 1.0])
 def test_q8_prefill_zipf_512(orc, engine, skew):
     """T=512 with Zipf-skewed routing (config 3): skew 0.13 puts ~60 tokens on
