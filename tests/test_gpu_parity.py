@@ -361,6 +361,18 @@ def test_every_token_same_experts(orc, engine, T, kind):
     assert np.array_equal(got.view(np.uint32), np.repeat(got[:1], T, axis=0).view(np.uint32)), "tokens differ"
 
 
+@pytest.mark.parametrize("T", [1, 3, 5, 64])
+@pytest.mark.parametrize("ne,k", [(8, 8), (4, 4), (32, 10), (64, 16)])
+def test_k_edges(orc, engine, ne, k, T):
+    """k at its edges: every expert chosen (k = n_expert: the routing has no
+    k+1-th expert to separate from), and k past the 8 of the fast top-k
+    network (10, 16: the routes by repeated maxima).  Against the oracle."""
+    print(f"case k edges ne={ne} k={k} T={T}", flush=True)
+    layer, moe = layer_for(engine, seed=85, n_expert=ne, k=k)
+    h = synth.make_tokens(960 + T, T, offsets=T > 1)
+    full_parity(orc, engine, layer, moe, h, block_dots=T == 5, min_exact=0.9999 if T < 64 else 0.0)
+
+
 @pytest.mark.parametrize("skew", [0.13, 1.0])
 def test_q8_prefill_zipf_512(orc, engine, skew):
     """T=512 with Zipf-skewed routing (config 3): skew 0.13 puts ~60 tokens on
