@@ -1494,6 +1494,7 @@ template <int TY, int K> struct Chain;
 // (quant.rs:1368-1382)
 template <int K> struct Chain<T_Q8_0, K> {
     static constexpr int S = K / 64;
+    static constexpr int NLOAD_MIN = S / 4; // vector loads of a load_chunk, at least
     int w[S];
     int hw[S / 2]; // the f16 scales, two per register
     // chunk c (elements cK .. cK + K - 1) of a row of KF elements: the
@@ -1525,6 +1526,7 @@ template <int K> struct Chain<T_Q8_0, K> {
 // of sub-block 2s + pi (quant.rs:1384-1423)
 template <int K> struct Chain<T_Q4K, K> {
     static constexpr int S = K / 64;
+    static constexpr int NLOAD_MIN = S / 4; // vector loads of a load_chunk, at least
     // the nibbles of steps 2m (low) and 2m + 1 (high) of each byte in wp[m];
     // per super-block its f32 d and the four sub-scales of this parity as
     // bytes: half the registers of whole words and f32 scales, for more
@@ -1579,6 +1581,7 @@ template <int K> struct Chain<T_Q4K, K> {
 // (quant.rs:1475-1533)
 template <int K> struct Chain<T_Q6K, K> {
     static constexpr int S = K / 64;
+    static constexpr int NLOAD_MIN = S / 4; // vector loads of a load_chunk, at least
     int ql[S / 2], qh[S / 2];
     int sc[S];
     float dd[S / 4];
@@ -1634,6 +1637,7 @@ template <int K> struct Chain<T_Q6K, K> {
 // holds elements L, L + 16, ... (layout.hpp bf16_elem), two per register.
 template <int K> struct Chain<T_BF16, K> {
     static constexpr int S = K / 16;
+    static constexpr int NLOAD_MIN = S / 8; // vector loads of a load_chunk, at least
     int w[S / 2];
     __device__ inline void load(const DevMat &M, size_t mrow, int pi, int l) { load_chunk(M, mrow, K, 0, pi, l); }
     __device__ inline void load_chunk(const DevMat &M, size_t mrow, int KF, int c, int pi, int l)
@@ -1820,7 +1824,7 @@ __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long_full(LongArgs a)
     constexpr int K = LK, S = K / 64, ROW16 = K / 16 + K / 128, NTH = WV * WAVE;
     constexpr bool BF = TY == T_BF16;
     constexpr int PIECES = BF ? XTT * K / 4 : XTT * ROW16; // 16-byte pieces of one chunk's rows (XTT rows)
-    extern __shared__ int4 dyn[];                          // [nc][PIECES]
+    extern __shared__ int4 dyn[];                          // [nc][nt rows of pieces]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane >> 4, ln = lane & 15, pi = ln >> 3, l = ln & 7;
     constexpr int RPW = GATEUP ? 2 : 4;
@@ -1836,13 +1840,13 @@ __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long_full(LongArgs a)
     const bool row_ok = row < rows;
     const size_t mrow = row_ok ? row : 0;
     const int t0 = blockIdx.y * XTT, nt = min(XTT, a.T - t0);
-    // the first weight chunks go out before the activations
-    Chain<TY, K> w[LPD];
-#pragma unroll
-    for (int d = 0; d < LPD; d++) w[d].load_chunk(M, mrow, KF, d < nc ? d : 0, pi, l);
-    // every chunk of the nt rows: piece (c, j, r) at dyn[c * PIECES + j * (BF ? K / 4 : ROW16) + r]
-    const int rp = BF ? K / 4 : ROW16, np = nt * rp;
-    for (int i = threadIdx.x; i < nc * np; i += NTH) {
+    // every chunk of the nt rows, piece (c, j, r) at dyn[c * np + j * rp + r],
+    // straight into LDS ahead of the weights (DMAs the compiler does not
+    // track: its waits for the weights then leave the activations alone)
+    const int rp = BF ? K / 4 : ROW16, np = nt * rp, npc = nc * np;
+    for (int i0 = 0; i0 < npc; i0 += NTH) {
+        const int i = i0 + (int)threadIdx.x;
+        if (i >= npc) break;
         const int c = i / np, jr = i - c * np, j = jr / rp, r = jr - j * rp;
         const void *src;
         if constexpr (BF) {
@@ -1856,10 +1860,16 @@ __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long_full(LongArgs a)
                 src = a.xd + x * (KF / 32) + ppi * (KF / 64) + (size_t)c * S + 4 * qq;
             }
         }
-        const int4 v = *reinterpret_cast<const int4 *>(src);
-        dyn[c * PIECES + jr] = v;
+        lds_dma16(static_cast<const float *>(src), reinterpret_cast<const float4 *>(dyn + i0 + wave * WAVE));
     }
-    __syncthreads();
+    // then the first weight chunks
+    Chain<TY, K> w[LPD];
+#pragma unroll
+    for (int d = 0; d < LPD; d++) w[d].load_chunk(M, mrow, KF, d < nc ? d : 0, pi, l);
+    // this thread's DMAs are in once at most the weights' loads are
+    // outstanding (loads complete in order); then every thread's
+    wait_vm<LPD * Chain<TY, K>::NLOAD_MIN>();
+    rm_barrier();
     float acc[XTT], mins[XTT];
 #pragma unroll
     for (int j = 0; j < XTT; j++) {
@@ -1867,7 +1877,7 @@ __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long_full(LongArgs a)
         mins[j] = 0.0f;
     }
     auto compute = [&](const Chain<TY, K> &wc, int c) {
-        const int4 *st = dyn + c * PIECES;
+        const int4 *st = dyn + c * np;
 #pragma unroll
         for (int j = 0; j < XTT; j++) {
             if (j >= nt) break;
