@@ -403,12 +403,17 @@ template <int N> __device__ inline void wait_vm()
 // writes, would otherwise wait for every DMA in flight before each LDS read
 // and undo the prefetch.  The caller waits for it with wait_vm.  (Writing m0
 // needs one wait state before the DMA reads it.)
-__device__ inline void lds_dma16(const float *g, const float4 *lds_dst)
+__device__ inline void lds_dma16_at(const void *g, unsigned lds_addr)
 {
-    const unsigned m0 = __builtin_amdgcn_readfirstlane(
-        (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)lds_dst);
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(lds_addr);
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
+// the LDS address (byte offset) of a shared-memory pointer
+__device__ inline unsigned lds_addr(const void *p)
+{
+    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+__device__ inline void lds_dma16(const float *g, const float4 *lds_dst) { lds_dma16_at(g, lds_addr(lds_dst)); }
 
 template <int NLD, int NW>
 __device__ inline void rm_issue(const float *wb, const float *xb, const unsigned (&off)[NLD], int st, float4 *base, int w)
@@ -1868,6 +1873,7 @@ __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long_full(LongArgs a)
     for (int d = 0; d < LPD; d++) w[d].load_chunk(M, mrow, KF, d < nc ? d : 0, pi, l);
     // this thread's DMAs are in once at most the weights' loads are
     // outstanding (loads complete in order); then every thread's
+    __builtin_amdgcn_sched_barrier(0); // (the weights' loads stay above the wait)
     wait_vm<LPD * Chain<TY, K>::NLOAD_MIN>();
     rm_barrier();
     float acc[XTT], mins[XTT];
@@ -2175,9 +2181,10 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
     __shared__ int4 stage[STAGE16 > RS16 ? STAGE16 : RS16]; // also the routing workgroup's scratch
     __shared__ int s_tok[MV_WAVES][GU_ROUTE_TMAX]; // ROUTE: the slot's tokens (staged rows), a copy per wave
     __shared__ int4 fstage[F32IN ? NPC * NTH : 1];
-    auto lds_load = [&](const void *src, int4 *dst_wave) {
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst_wave, 16, 0, 0);
-    };
+    // (inline asm: the compiler does not track these DMAs, so its waits for
+    // the weights do not cover them; the chunk loop waits for them itself)
+    const unsigned stage_a = lds_addr(stage), fstage_a = lds_addr(fstage);
+    auto lds_load = [&](const void *src, unsigned dst_wave) { lds_dma16_at(src, dst_wave); };
     // issue the loads of the nt rows of the chunk at i0 (row numbers of the
     // first chunk from the slot record: scalar loads, which do not wait on
     // vector loads); pieces past the chunk reread a valid row into unused LDS
@@ -2202,7 +2209,7 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
                 int xr = trow[0];
 #pragma unroll
                 for (int jj = 1; jj < XC; jj++) xr = jr == jj ? trow[jj] : xr;
-                lds_load(a.xf + (size_t)xr * K + 4 * (idx - jr * (K / 4)), &fstage[c * NTH + wave * WAVE]);
+                lds_load(a.xf + (size_t)xr * K + 4 * (idx - jr * (K / 4)), fstage_a + 16 * (c * NTH + wave * WAVE));
             }
         } else {
 #pragma unroll
@@ -2216,7 +2223,7 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
                 // quant pieces, then scale pieces (16 bytes each)
                 const uint8_t *src = r < K / 16 ? reinterpret_cast<const uint8_t *>(a.xq) + (size_t)xr * K + 16 * r
                                                 : reinterpret_cast<const uint8_t *>(a.xd) + (size_t)xr * (K / 8) + 16 * (r - K / 16);
-                lds_load(src, &stage[c * NTH + wave * WAVE]);
+                lds_load(src, stage_a + 16 * (c * NTH + wave * WAVE));
             }
         }
     };
@@ -2351,7 +2358,16 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
     for (int i0 = 0; i0 < cnt; i0 += XC) {
         const int nt = min(XC, cnt - i0);
         if (i0 > 0) issue_chunk(i0, nt);
-        __syncthreads();
+        // The chunk's rows are in once at most the loads issued after them
+        // are outstanding (loads complete in order): for the first chunk the
+        // weights' (so that the chains start while the later weights still
+        // arrive), for the others none.  The waits are explicit: the DMAs
+        // are inline asm, which the compiler's own waits (those of
+        // __syncthreads included) do not count.
+        __builtin_amdgcn_sched_barrier(0); // (the weights' loads stay above the wait)
+        if (i0 == 0) wait_vm<NSET * Chain<TY, K>::NLOAD_MIN>();
+        else wait_vm<0>();
+        rm_barrier();
         if constexpr (QX) {
             // one thread per 32-element block of the chunk
             const int b = threadIdx.x;
