@@ -162,6 +162,36 @@ __device__ inline void load32(const float *p, float (&v)[32])
     }
 }
 
+// s_waitcnt for at most N vector memory operations outstanding (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left free)
+template <int N> __device__ inline void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// One 16-byte-per-lane global -> LDS load (LDS address m0 + 16 lane), in
+// inline asm: the compiler, which cannot tell which stage buffer an LDS DMA
+// writes, would otherwise wait for every DMA in flight before each LDS read
+// and undo the prefetch.  The caller waits for it with wait_vm.  (Writing m0
+// needs one wait state before the DMA reads it.)
+__device__ inline void lds_dma16_at(const void *g, unsigned lds_addr)
+{
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(lds_addr);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+}
+// the LDS address (byte offset) of a shared-memory pointer
+__device__ inline unsigned lds_addr(const void *p)
+{
+    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+__device__ inline void lds_dma16(const float *g, const float4 *lds_dst) { lds_dma16_at(g, lds_addr(lds_dst)); }
+
+// a workgroup barrier with no memory fence: the callers order their LDS
+// themselves (their loads' waits), and a fence would also wait for every
+// load and store in flight
+__device__ inline void rm_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 // ---------------------------------------------------------------------------
 // Router logits (and the shared expert's gate logit, row n_expert) in the
 // order of biv's AVX2 dot_f32 (quant.rs:1177-1207): lane L of a 32-lane half
@@ -248,6 +278,24 @@ template <int NS, int TC, int NTH = 256> __global__ __launch_bounds__(NTH) void 
     const bool valid = row < n_expert || (row == n_expert && a.gate_inp != nullptr);
     // gate_inp as an offset from the router: one pointer, a per-lane offset
     const float *w = router + (row < n_expert ? (ptrdiff_t)row * E : (valid ? a.gate_inp - router : 0));
+    // this workgroup's tokens into LDS first (row-major, straight from
+    // global memory by DMAs the compiler does not track; pieces past the
+    // last token reread it into unused LDS), then the row into registers:
+    // the chains start once the tokens are in, the row's later words still
+    // arriving
+    __shared__ float xs[TC][E];
+    const int t0 = blockIdx.y * TC, nt = min(TC, T - t0);
+    {
+        constexpr int NP = TC * (E / 4) / NTH; // 16-byte pieces per thread
+        const float4 *src = reinterpret_cast<const float4 *>(h + (size_t)t0 * E);
+        const unsigned dst = lds_addr(&xs[0][0]) + 16 * (threadIdx.x & ~(WAVE - 1));
+#pragma unroll
+        for (int c = 0; c < NP; c++) {
+            if (c * NTH >= nt * (E / 4)) break; // uniform
+            const int idx0 = c * NTH + (int)threadIdx.x, idx = idx0 < nt * (E / 4) ? idx0 : nt * (E / 4) - 1;
+            lds_dma16_at(src + idx, dst + 16 * c * NTH);
+        }
+    }
     float wv[NS];
     {
         const float4 *p = reinterpret_cast<const float4 *>(w);
@@ -260,30 +308,18 @@ template <int NS, int TC, int NTH = 256> __global__ __launch_bounds__(NTH) void 
             wv[4 * i + 3] = v.w;
         }
     }
-    // this workgroup's tokens into LDS (row-major, straight from global
-    // memory; pieces past the last token reread it into unused LDS)
-    __shared__ float xs[TC][E];
-    const int t0 = blockIdx.y * TC, nt = min(TC, T - t0);
-    // post_norm: this thread's norm weights, loaded while the tokens stage
+    // post_norm: this thread's norm weights
     constexpr int NWPT = E / NTH > 0 ? E / NTH : 1;
     float nw[NWPT];
     if (a.norm_w) {
 #pragma unroll
         for (int j = 0; j < NWPT; j++) nw[j] = (int)threadIdx.x + NTH * j < E ? a.norm_w[threadIdx.x + NTH * j] : 0.0f;
     }
-    {
-        constexpr int NP = TC * (E / 4) / NTH; // 16-byte pieces per thread
-        const float4 *src = reinterpret_cast<const float4 *>(h + (size_t)t0 * E);
-        float4 *dst = reinterpret_cast<float4 *>(&xs[0][0]) + (threadIdx.x & ~(WAVE - 1));
-#pragma unroll
-        for (int c = 0; c < NP; c++) {
-            if (c * NTH >= nt * (E / 4)) break; // uniform
-            const int idx0 = c * NTH + (int)threadIdx.x, idx = idx0 < nt * (E / 4) ? idx0 : nt * (E / 4) - 1;
-            __builtin_amdgcn_global_load_lds(src + idx, (__attribute__((address_space(3))) void *)(dst + c * NTH), 16, 0,
-                                             0);
-        }
-    }
-    __syncthreads();
+    // the tokens are in once at most the row's loads are outstanding (loads
+    // complete in order); then every thread's
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm<NS / 4>();
+    rm_barrier();
     if (a.norm_w) {
         // rms_norm of the staged tokens in place: a half wave per token forms
         // the scale, then every thread scales its elements, v * (scale * w)
@@ -386,35 +422,10 @@ constexpr int RM_NTH = 512;
 template <int SH, int MI> constexpr int rm_tokens() { return 32 * (MI / 2); }
 template <int SH, int MI> constexpr int rm_nbuf() { return SH == 32 && MI == 4 ? 3 : 4; }
 
-// s_waitcnt for at most N vector memory operations outstanding (gfx9
-// encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left free)
-template <int N> __device__ inline void wait_vm()
-{
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 // stage st of a thread's NLD words: word q * RM_NTH + tid lands at that
 // index of the buffer (global_load_lds writes a wave's 64 words in lane
 // order); the first NW are router words (offsets from wb), the rest token
 // words (from xb)
-// One 16-byte-per-lane global -> LDS load (LDS address m0 + 16 lane), in
-// inline asm: the compiler, which cannot tell which stage buffer an LDS DMA
-// writes, would otherwise wait for every DMA in flight before each LDS read
-// and undo the prefetch.  The caller waits for it with wait_vm.  (Writing m0
-// needs one wait state before the DMA reads it.)
-__device__ inline void lds_dma16_at(const void *g, unsigned lds_addr)
-{
-    const unsigned m0 = __builtin_amdgcn_readfirstlane(lds_addr);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
-}
-// the LDS address (byte offset) of a shared-memory pointer
-__device__ inline unsigned lds_addr(const void *p)
-{
-    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-__device__ inline void lds_dma16(const float *g, const float4 *lds_dst) { lds_dma16_at(g, lds_addr(lds_dst)); }
-
 template <int NLD, int NW>
 __device__ inline void rm_issue(const float *wb, const float *xb, const unsigned (&off)[NLD], int st, float4 *base, int w)
 {
@@ -422,9 +433,6 @@ __device__ inline void rm_issue(const float *wb, const float *xb, const unsigned
     for (int q = 0; q < NLD; q++) lds_dma16((q < NW ? wb : xb) + off[q] + 128 * st, base + q * RM_NTH + w * WAVE);
 }
 
-// a workgroup barrier with no memory fence: the stage loop orders its LDS
-// itself (its loads' waits), and a fence would also wait for the stores in flight
-__device__ inline void rm_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // slot of a workgroup's tile: the tiles are dealt round-robin over the 8
 // XCDs by workgroup id, so give XCD x a run of consecutive tiles (row tiles
@@ -2639,7 +2647,7 @@ __global__ __launch_bounds__(DC_WAVES *WAVE) void k_down_combine(DcArgs a)
     const bool cmine = tid < T * DC_RB;
     float *const cpo = a.out + (size_t)ct * rows + row0 + cr;
     const float cres = a.add && cmine ? *cpo : 0.0f;
-    if (tid < 32) tab[tid] = exp_tab_g[tid];
+    const uint64_t tv = tid < 32 ? exp_tab_g[tid] : 0ull; // into LDS at the end (a store now would wait for it)
     // the intermediate, quantised into LDS: one 32-element block per thread and turn
     if (tid < nblk)
         quant_block_at(v0, K, tid % (K / 32), reinterpret_cast<int *>(&stage[(tid / (K / 32)) * ROW16]),
@@ -2651,7 +2659,10 @@ __global__ __launch_bounds__(DC_WAVES *WAVE) void k_down_combine(DcArgs a)
         quant_block_at(v, K, bb, reinterpret_cast<int *>(&stage[r * ROW16]),
                        reinterpret_cast<float *>(&stage[r * ROW16 + K / 16]), nullptr);
     }
-    __syncthreads();
+    // the quantised rows are in LDS once this thread's writes are done; a
+    // bare barrier (__syncthreads would also wait for the weights in flight)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    rm_barrier();
     const float cw = tid < nc ? a.dp.pair_w[cp] : 0.0f; // consumed after the rows
     for (int i0 = 0; i0 < per; i0 += DC_D) {
 #pragma unroll
@@ -2698,6 +2709,8 @@ __global__ __launch_bounds__(DC_WAVES *WAVE) void k_down_combine(DcArgs a)
         cpos[tid] = cp;
         cwt[tid] = cw;
     }
+    if (tid < 32) tab[tid] = tv; // wave 0, which alone reads it
+    wave_lds_sync();
     if (has_shared && tid < T) csig[tid] = 1.0f / (1.0f + exp_lds(-cg, tab)); // ops::sigmoid
     __syncthreads();
     // the combine of this workgroup's rows: fma(w, y, o) over the token's
