@@ -163,7 +163,6 @@ __device__ inline void load32(const float *p, float (&v)[32])
     }
 }
 
-
 // ---------------------------------------------------------------------------
 // Router logits (and the shared expert's gate logit, row n_expert) in the
 // order of biv's AVX2 dot_f32 (quant.rs:1177-1207): lane L of a 32-lane half
@@ -404,7 +403,6 @@ __device__ inline void rm_issue(const float *wb, const float *xb, const unsigned
 #pragma unroll
     for (int q = 0; q < NLD; q++) lds_dma16((q < NW ? wb : xb) + off[q] + 128 * st, base + q * RM_NTH + w * WAVE);
 }
-
 
 // slot of a workgroup's tile: the tiles are dealt round-robin over the 8
 // XCDs by workgroup id, so give XCD x a run of consecutive tiles (row tiles
@@ -1808,8 +1806,7 @@ __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long_full(LongArgs a)
     constexpr int LPD = long_lpd<XTT, GATEUP>();
     constexpr int K = LK, S = K / 64, ROW16 = K / 16 + K / 128, NTH = WV * WAVE;
     constexpr bool BF = TY == T_BF16;
-    constexpr int PIECES = BF ? XTT * K / 4 : XTT * ROW16; // 16-byte pieces of one chunk's rows (XTT rows)
-    extern __shared__ int4 dyn[];                          // [nc][nt rows of pieces]
+    extern __shared__ int4 dyn[]; // [nc chunks][nt rows][16-byte pieces of a chunk's row]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = lane >> 4, ln = lane & 15, pi = ln >> 3, l = ln & 7;
     constexpr int RPW = GATEUP ? 2 : 4;
@@ -2631,8 +2628,8 @@ __global__ __launch_bounds__(DC_WAVES *WAVE) void k_down_combine(DcArgs a)
         quant_block_at(v, K, bb, reinterpret_cast<int *>(&stage[r * ROW16]),
                        reinterpret_cast<float *>(&stage[r * ROW16 + K / 16]), nullptr);
     }
-    // the quantised rows are in LDS once this thread's writes are done; a
-    // bare barrier (__syncthreads would also wait for the weights in flight)
+    // the quantised rows are in LDS once this thread's writes are done: a
+    // bare barrier after them, which leaves the weights in flight alone
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     rm_barrier();
     const float cw = tid < nc ? a.dp.pair_w[cp] : 0.0f; // consumed after the rows
