@@ -1040,8 +1040,13 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
         // steps for Q8_0, measured slower); the last turn reloads its own step
         // rather than branch
         typename W::Step w1;
+        // the step count as a value the compiler cannot see through (a.T is
+        // never negative): narrow rows give a loop of one or two turns,
+        // which it would otherwise lay out flat, with the turns' loads and
+        // chains overlapped past the registers
+        const int nsteps = W::STEPS + (a.T < 0 ? 2 : 0);
 #pragma unroll 1
-        for (int h = 0; h < W::STEPS; h += 2) {
+        for (int h = 0; h < nsteps; h += 2) {
             wsrc.load(h + 1, w1);
             stepc(h, std::integral_constant<int, 0>(), w0);
             wsrc.load(min(h + 2, W::STEPS - 2), w0);
