@@ -1464,6 +1464,22 @@ __global__ __launch_bounds__(RS_THREADS) void k_route_sort(const float *__restri
     route_block_counts(dp.ids, n_expert, k, T, blockIdx.x, work);
 }
 
+// The x86 kernels' tree over the 16 chains of a (row, token) that a 16-lane
+// group of the chain kernels holds, lane by lane acc0 + acc1, the two
+// 128-bit halves, movehl, movehdup (partners 8, 4, 2 and 1 lanes on), into
+// the group's first lane (the other lanes' results are not used): DPP
+// row_shl moves within the 16-lane row, not LDS permutes.
+#define BIV_ROW_SHL(x, n) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + (n), 0xF, 0xF, true))
+__device__ inline float row_tree16(float acc)
+{
+    float t = acc + BIV_ROW_SHL(acc, 8); // acc0 + acc1, lane by lane
+    t = t + BIV_ROW_SHL(t, 4);           // the two 128-bit halves
+    t = t + BIV_ROW_SHL(t, 2);           // movehl
+    t = t + BIV_ROW_SHL(t, 1);           // movehdup
+    return t;
+}
+#undef BIV_ROW_SHL
+
 // ---------------------------------------------------------------------------
 // Expert rows as 16 FMA chains.  Chain<TY, K> holds, in registers, what lane
 // (pi, l) of a 16-lane group needs of one weight row: word l of the blocks of
@@ -1898,10 +1914,7 @@ __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long_full(LongArgs a)
 #pragma unroll
     for (int j = 0; j < XTT; j++) {
         if (j >= nt) break;
-        float t = acc[j] + __shfl_xor(acc[j], 8); // acc0 + acc1, lane by lane
-        t = t + __shfl_xor(t, 4);                 // the two 128-bit halves
-        t = t + __shfl_xor(t, 2);                 // movehl
-        t = t + __shfl_xor(t, 1);                 // movehdup
+        float t = row_tree16(acc[j]); // valid in the group's first lane
         if (TY == T_Q4K) t = t - __shfl(mins[j], lane & ~15);
         const size_t o = (size_t)(t0 + j) * rows + row;
         if (GATEUP) {
@@ -2016,10 +2029,7 @@ __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long(LongArgs a)
 #pragma unroll
     for (int j = 0; j < XTT; j++) {
         if (j >= nt) break;
-        float t = acc[j] + __shfl_xor(acc[j], 8); // acc0 + acc1, lane by lane
-        t = t + __shfl_xor(t, 4);                 // the two 128-bit halves
-        t = t + __shfl_xor(t, 2);                 // movehl
-        t = t + __shfl_xor(t, 1);                 // movehdup
+        float t = row_tree16(acc[j]); // valid in the group's first lane
         if (TY == T_Q4K) t = t - __shfl(mins[j], lane & ~15);
         const size_t o = (size_t)(t0 + j) * rows + row;
         if (GATEUP) {
@@ -2368,10 +2378,7 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
                     float acc = 0.0f;
 #pragma unroll
                     for (int s = 0; s < K / 16; s++) acc = fmaf(wc[q].wval(s), xr[16 * s + ln], acc);
-                    float t = acc + __shfl_xor(acc, 8); // acc0 + acc1, lane by lane
-                    t = t + __shfl_xor(t, 4);           // the two 128-bit halves
-                    t = t + __shfl_xor(t, 2);           // movehl
-                    t = t + __shfl_xor(t, 1);           // movehdup
+                    float t = row_tree16(acc); // valid in the group's first lane
                     if (GATEUP) {
                         const float up = __shfl_xor(t, 16);
                         if (m == 0 && ln == 0 && row_ok) a.out[orow * rows + row] = silu_mul(t, up);
@@ -2421,10 +2428,7 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
                         if (dump && l == 0 && row_ok) dump[(orow * rows + row) * (K / 32) + 2 * s + pi] = bs;
                     }
                 }
-                float t = acc + __shfl_xor(acc, 8); // acc0 + acc1, lane by lane
-                t = t + __shfl_xor(t, 4);           // the two 128-bit halves
-                t = t + __shfl_xor(t, 2);           // movehl
-                t = t + __shfl_xor(t, 1);           // movehdup
+                float t = row_tree16(acc); // valid in the group's first lane
                 if (TY == T_Q4K) t = t - q4k_mins_group<K>(M, (size_t)e * rows + (row_ok ? row : 0), a.xs, xrow, ln);
                 if (GATEUP) {
                     const float up = __shfl_xor(t, 16);
@@ -2664,10 +2668,7 @@ __global__ __launch_bounds__(DC_WAVES *WAVE) void k_down_combine(DcArgs a)
                             }
                         }
                     }
-                    float t = acc + __shfl_xor(acc, 8); // acc0 + acc1, lane by lane
-                    t = t + __shfl_xor(t, 4);           // the two 128-bit halves
-                    t = t + __shfl_xor(t, 2);           // movehl
-                    t = t + __shfl_xor(t, 1);           // movehdup
+                    float t = row_tree16(acc); // valid in the group's first lane
                     if (ln == 0) ylds[orow * DC_RB + (r - row0)] = t;
                 }
             }
