@@ -163,6 +163,42 @@ __device__ inline void load32(const float *p, float (&v)[32])
     }
 }
 
+// The x86 kernels' tree over the 16 chains of a (row, token) that a 16-lane
+// group of the chain kernels holds, lane by lane acc0 + acc1, the two
+// 128-bit halves, movehl, movehdup (partners 8, 4, 2 and 1 lanes on), into
+// the group's first lane (the other lanes' results are not used): DPP
+// row_shl moves within the 16-lane row, not LDS permutes.
+#define BIV_ROW_SHL(x, n) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + (n), 0xF, 0xF, true))
+__device__ inline float row_tree16(float acc)
+{
+    float t = acc + BIV_ROW_SHL(acc, 8); // acc0 + acc1, lane by lane
+    t = t + BIV_ROW_SHL(t, 4);           // the two 128-bit halves
+    t = t + BIV_ROW_SHL(t, 2);           // movehl
+    t = t + BIV_ROW_SHL(t, 1);           // movehdup
+    return t;
+}
+// The same tree for the 32 chains of dot_f32 on a 32-lane half wave
+// (quant.rs:1149-1153): lanes 8 apart (acc0 + acc1, acc2 + acc3), then 16
+// ((acc0 + acc1) + (acc2 + acc3)), then 4, 2, 1; into lane 0 of the half
+__device__ inline float half_tree32(float v)
+{
+    v = v + BIV_ROW_SHL(v, 8);
+    v = v + __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
+    v = v + BIV_ROW_SHL(v, 4);
+    v = v + BIV_ROW_SHL(v, 2);
+    v = v + BIV_ROW_SHL(v, 1);
+    return v;
+}
+#undef BIV_ROW_SHL
+
+// lane l's x from lane l + 16 (lanes 0-15 and 32-47, the first groups of
+// each 32-lane half: v_permlane16_swap, not an LDS permute)
+__device__ inline float from_lane_plus16(float x)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[1]);
+}
+
 // ---------------------------------------------------------------------------
 // Router logits (and the shared expert's gate logit, row n_expert) in the
 // order of biv's AVX2 dot_f32 (quant.rs:1177-1207): lane L of a 32-lane half
@@ -315,12 +351,7 @@ template <int NS, int TC, int NTH = 256> __global__ __launch_bounds__(NTH) void 
         __syncthreads();
     }
     auto finish = [&](float acc, int t) {
-        float v = acc;
-        v = v + __shfl_xor(v, 8);  // acc0+acc1 (lanes 0-7), acc2+acc3 (16-23)
-        v = v + __shfl_xor(v, 16); // (acc0+acc1)+(acc2+acc3)
-        v = v + __shfl_xor(v, 4);  // the two 128-bit halves
-        v = v + __shfl_xor(v, 2);  // movehl
-        v = v + __shfl_xor(v, 1);  // movehdup
+        const float v = half_tree32(acc); // valid in lane 0 of the half wave
         if (valid && L == 0) {
             if (row < n_expert) a.logits[(size_t)t * n_expert + row] = v;
             else a.glogit[t] = v;
@@ -1464,22 +1495,6 @@ __global__ __launch_bounds__(RS_THREADS) void k_route_sort(const float *__restri
     route_block_counts(dp.ids, n_expert, k, T, blockIdx.x, work);
 }
 
-// The x86 kernels' tree over the 16 chains of a (row, token) that a 16-lane
-// group of the chain kernels holds, lane by lane acc0 + acc1, the two
-// 128-bit halves, movehl, movehdup (partners 8, 4, 2 and 1 lanes on), into
-// the group's first lane (the other lanes' results are not used): DPP
-// row_shl moves within the 16-lane row, not LDS permutes.
-#define BIV_ROW_SHL(x, n) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + (n), 0xF, 0xF, true))
-__device__ inline float row_tree16(float acc)
-{
-    float t = acc + BIV_ROW_SHL(acc, 8); // acc0 + acc1, lane by lane
-    t = t + BIV_ROW_SHL(t, 4);           // the two 128-bit halves
-    t = t + BIV_ROW_SHL(t, 2);           // movehl
-    t = t + BIV_ROW_SHL(t, 1);           // movehdup
-    return t;
-}
-#undef BIV_ROW_SHL
-
 // ---------------------------------------------------------------------------
 // Expert rows as 16 FMA chains.  Chain<TY, K> holds, in registers, what lane
 // (pi, l) of a 16-lane group needs of one weight row: word l of the blocks of
@@ -1915,10 +1930,10 @@ __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long_full(LongArgs a)
     for (int j = 0; j < XTT; j++) {
         if (j >= nt) break;
         float t = row_tree16(acc[j]); // valid in the group's first lane
-        if (TY == T_Q4K) t = t - __shfl(mins[j], lane & ~15);
+        if (TY == T_Q4K) t = t - mins[j]; // (the first lane formed it)
         const size_t o = (size_t)(t0 + j) * rows + row;
         if (GATEUP) {
-            const float up = __shfl_xor(t, 16);
+            const float up = from_lane_plus16(t); // (read by the gate groups' first lanes)
             if (m == 0 && ln == 0 && row_ok) a.out[o] = silu_mul(t, up);
         } else if (ln == 0 && row_ok) {
             a.out[o] = a.add ? a.out[o] + t : t;
@@ -2030,10 +2045,10 @@ __global__ __launch_bounds__(WV *WAVE) void k_chain_mv_long(LongArgs a)
     for (int j = 0; j < XTT; j++) {
         if (j >= nt) break;
         float t = row_tree16(acc[j]); // valid in the group's first lane
-        if (TY == T_Q4K) t = t - __shfl(mins[j], lane & ~15);
+        if (TY == T_Q4K) t = t - mins[j]; // (the first lane formed it)
         const size_t o = (size_t)(t0 + j) * rows + row;
         if (GATEUP) {
-            const float up = __shfl_xor(t, 16);
+            const float up = from_lane_plus16(t); // (read by the gate groups' first lanes)
             if (m == 0 && ln == 0 && row_ok) a.out[o] = silu_mul(t, up);
         } else if (ln == 0 && row_ok) {
             a.out[o] = a.add ? a.out[o] + t : t;
@@ -2380,7 +2395,7 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
                     for (int s = 0; s < K / 16; s++) acc = fmaf(wc[q].wval(s), xr[16 * s + ln], acc);
                     float t = row_tree16(acc); // valid in the group's first lane
                     if (GATEUP) {
-                        const float up = __shfl_xor(t, 16);
+                        const float up = from_lane_plus16(t); // (read by the gate groups' first lanes)
                         if (m == 0 && ln == 0 && row_ok) a.out[orow * rows + row] = silu_mul(t, up);
                     } else {
                         if (ln == 0 && row_ok) a.out[orow * rows + row] = t;
@@ -2431,7 +2446,7 @@ __global__ __launch_bounds__(MV_WAVES *WAVE) __attribute__((amdgpu_waves_per_eu(
                 float t = row_tree16(acc); // valid in the group's first lane
                 if (TY == T_Q4K) t = t - q4k_mins_group<K>(M, (size_t)e * rows + (row_ok ? row : 0), a.xs, xrow, ln);
                 if (GATEUP) {
-                    const float up = __shfl_xor(t, 16);
+                    const float up = from_lane_plus16(t); // (read by the gate groups' first lanes)
                     if (m == 0 && ln == 0 && row_ok) a.out[orow * rows + row] = silu_mul(t, up);
                 } else {
                     if (ln == 0 && row_ok) a.out[orow * rows + row] = t;
