@@ -627,6 +627,21 @@ __device__ inline float ordered_to_f32(unsigned u) { return __uint_as_float(u & 
 
 // Max over the wavefront of an unsigned value, in every lane: DPP within
 // rows of 16 lanes, then the four row results through scalar registers.
+// Inclusive prefix sum of v over the wavefront's 64 lanes by DPP: shifts
+// of 1, 2, 4, 8 within each row of 16, then row 0's and row 2's totals into
+// rows 1 and 3 (row_bcast:15) and rows 0-1's total into rows 2-3
+// (row_bcast:31); lanes a shift leaves without a source add 0
+__device__ inline int wave_incl_scan(int v)
+{
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false); // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false); // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false); // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false); // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false); // row_bcast:15 into rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false); // row_bcast:31 into rows 2, 3
+    return v;
+}
+
 __device__ inline unsigned wave_max_u32(unsigned v)
 {
     v = max(v, (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
@@ -1114,16 +1129,8 @@ __device__ void sort_pairs_wave(const int *ids, const float *wts, int n_expert, 
         tot += c[j];
         stot += ns[j];
     }
-    int x = tot, y = stot;
-#pragma unroll
-    for (int off = 1; off < WAVE; off <<= 1) {
-        const int xs = __shfl_up(x, off), ys = __shfl_up(y, off);
-        if (lane >= off) {
-            x += xs;
-            y += ys;
-        }
-    }
-    const int n_used = __shfl(y, WAVE - 1);
+    const int x = wave_incl_scan(tot), y = wave_incl_scan(stot);
+    const int n_used = __builtin_amdgcn_readlane(y, WAVE - 1);
     int pos = x - tot, spos = y - stot;
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
