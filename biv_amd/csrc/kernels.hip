@@ -802,11 +802,7 @@ template <int NS> __global__ __launch_bounds__(64 * PREP_TOK) void k_prep(Router
         float acc = 0.0f;
 #pragma unroll
         for (int k = 0; k < NS; k++) acc = fmaf(wg[L + 32 * k], v[k], acc);
-        acc = acc + __shfl_xor(acc, 8);
-        acc = acc + __shfl_xor(acc, 16);
-        acc = acc + __shfl_xor(acc, 4);
-        acc = acc + __shfl_xor(acc, 2);
-        acc = acc + __shfl_xor(acc, 1);
+        acc = half_tree32(acc); // valid in lane 0
         if (lane == 0) a.glogit[t] = acc;
     }
     float *r = &rows[w][0];
@@ -1268,16 +1264,7 @@ __device__ inline void expert_scan(int tot, int chunk, bool writer, int (&wsum)[
     const int lane = threadIdx.x & (WAVE - 1), w = (threadIdx.x & (MAX_EXPERTS - 1)) >> 6;
     const int nsl = (tot + chunk - 1) / chunk;
     const bool light = tot > 0 && 2 * tot <= chunk;
-    int x = tot, yh = light ? 0 : nsl, yl = light ? nsl : 0;
-#pragma unroll
-    for (int off = 1; off < WAVE; off <<= 1) {
-        const int xs = __shfl_up(x, off), hs = __shfl_up(yh, off), ls = __shfl_up(yl, off);
-        if (lane >= off) {
-            x += xs;
-            yh += hs;
-            yl += ls;
-        }
-    }
+    const int x = wave_incl_scan(tot), yh = wave_incl_scan(light ? 0 : nsl), yl = wave_incl_scan(light ? nsl : 0);
     if (writer && lane == WAVE - 1) {
         wsum[0][w] = x;
         wsum[1][w] = yh;
