@@ -18,7 +18,10 @@ template <int N> __device__ inline void wait_vm()
 // inline asm: the compiler, which cannot tell which stage buffer an LDS DMA
 // writes, would otherwise wait for every DMA in flight before each LDS read
 // and undo the prefetch.  The caller waits for it with wait_vm.  (Writing m0
-// needs one wait state before the DMA reads it.)
+// needs one wait state before the DMA reads it.  The compiler does not save
+// m0 around the asm; no kernel that calls this also uses
+// __builtin_amdgcn_global_load_lds or anything else for which the compiler
+// keeps a value in m0, which the assembly of every kernel shows.)
 __device__ inline void lds_dma16_at(const void *g, unsigned lds_addr)
 {
     const unsigned m0 = __builtin_amdgcn_readfirstlane(lds_addr);
