@@ -51,7 +51,7 @@ def check(ref, got, min_exact=0.9999):
     assert exact >= min_exact
 
 
-@pytest.mark.parametrize("T", [1, 5, 9, 40])
+@pytest.mark.parametrize("T", [1, 2, 3, 5, 8, 9, 17, 40, 64, 130])
 def test_dense_q8(orc, engine, T):
     print(f"case dense q8 T={T}", flush=True)
     layer, d = dense_for(engine, seed=11, n_embd=2048, n_ff=3584)
@@ -71,11 +71,13 @@ def test_dense_types(orc, engine, types):
 
 
 def test_dense_large_rows(orc, engine):
-    """A qwen35 9B-sized FFN: n_embd 4096, n_ff 12288 (24 chunks per down row)."""
+    """A qwen35 9B-sized FFN: n_embd 4096, n_ff 12288 (24 chunks per down row),
+    at 2, 5 and 8 tokens (each workgroup's tokens and weight ring differ)."""
     print("case dense 4096 x 12288", flush=True)
     layer, d = dense_for(engine, seed=13, n_embd=4096, n_ff=12288)
-    h = synth.make_tokens(800, 2, n_embd=4096)
-    check(reference(orc, layer, h), d.ffn(h))
+    for T in (2, 5, 8):
+        h = synth.make_tokens(800 + T, T, n_embd=4096)
+        check(reference(orc, layer, h), d.ffn(h))
 
 
 def test_dense_add_and_device(orc, engine):
@@ -117,6 +119,8 @@ def test_dense_errors(engine):
     assert rc == -2 and "one type" in engine.L.biv_hip_last_error(engine.h).decode()
     rc = engine.L.biv_hip_dense_create(engine.h, g, g, bad, ctypes.byref(out))
     assert rc == -1 and "shapes" in engine.L.biv_hip_last_error(engine.h).decode()
+    layer, d = dense_for(engine, seed=11, n_embd=2048, n_ff=3584)
+    assert d.ffn(np.zeros((0, 2048), np.float32)).shape == (0, 2048)
 
 
 def test_dense_from_gguf(orc, engine, tmp_path):
