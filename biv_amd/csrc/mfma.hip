@@ -1090,7 +1090,8 @@ __global__ __launch_bounds__(GNTH) __attribute__((amdgpu_waves_per_eu(DUMP ? 1 :
 // 2 t + hh, column n is dot16_hh of input row t and weight row n, exactly,
 // and lane (n, kq) holds both halves of input rows 2 kq and 2 kq + 1: isum
 // in integers, then the f32 scaling; the sum over blocks runs in an order of
-// its own (down's outputs only meet the combine).
+// its own (down's outputs only meet the combine): d_x * isum summed over a
+// super-block's eight blocks, times its d once.
 //
 // Weights (chain layout, layout.hpp): per 512 elements (four halves qq of a
 // row) the ql units 16 (qq / 4) + 8 pi + w hold ql word w of quarters pi and
@@ -1180,7 +1181,9 @@ __global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
     // lanes kq = 2 hh and 2 hh + 1 hold
     const uint32_t keep = ((n & 1) == (kq >> 1)) ? ~0u : 0u;
     const int at = n >> 1; // A row's input row within the 8-row group
-    float acc[QT / 8][RT][2];
+    // acc: the sum over super-blocks of d * (the super-block's sum over its
+    // blocks of d_x * isum, in asb)
+    float acc[QT / 8][RT][2], asb[QT / 8][RT][2];
 #pragma unroll
     for (int t = 0; t < QT / 8; t++)
 #pragma unroll
@@ -1229,9 +1232,13 @@ __global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
                     // sub-scales int8): the same integers as 32-bit ones
                     const int is0 = __mul24(sc0[r], d[0]) + __mul24(sc1[r], d[1]);
                     const int is1 = __mul24(sc0[r], d[2]) + __mul24(sc1[r], d[3]);
-                    const float dd = dsb[r][qq >> 1];
-                    acc[t][r][0] = __builtin_fmaf((float)is0, dd * dx.x, acc[t][r][0]);
-                    acc[t][r][1] = __builtin_fmaf((float)is1, dd * dx.y, acc[t][r][1]);
+                    asb[t][r][0] = (bl & 7) ? __builtin_fmaf((float)is0, dx.x, asb[t][r][0]) : (float)is0 * dx.x;
+                    asb[t][r][1] = (bl & 7) ? __builtin_fmaf((float)is1, dx.y, asb[t][r][1]) : (float)is1 * dx.y;
+                    if ((bl & 7) == 7) {
+                        const float dd = dsb[r][qq >> 1];
+                        acc[t][r][0] = __builtin_fmaf(dd, asb[t][r][0], acc[t][r][0]);
+                        acc[t][r][1] = __builtin_fmaf(dd, asb[t][r][1], acc[t][r][1]);
+                    }
                     if (DUMP && a.dump_a) { // the block int32s, for the taps
                         const int i0 = 8 * t + 2 * kq, row = rw0 + 16 * r + n;
                         if (i0 < cnt) a.dump_a[((size_t)(beg + i0) * rows + row) * NB + b] = is0;
