@@ -1106,7 +1106,7 @@ __global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
     constexpr int XSTR = K / 16 + 1; // staged quant row: 16-byte units (+1 against bank conflicts)
     constexpr int DSTR = QT + 4;     // staged scales [block][pair], floats
     static_assert(K % 512 == 0 && QT % 8 == 0, "shapes");
-    __shared__ uint4 xq_s[QT * XSTR];
+    __shared__ uint4 xq_s[(QT + 1) * XSTR]; // the slot's rows, then a row of zeros
     __shared__ float xd_s[NB * DSTR];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, kq = lane >> 4;
@@ -1169,6 +1169,7 @@ __global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
             const size_t ar = beg + min(i, cnt - 1);
             xq_s[i * XSTR + c] = reinterpret_cast<const uint4 *>(a.xq + ar * K)[c];
         }
+        for (int c = tid; c < XSTR; c += QNTH) xq_s[QT * XSTR + c] = make_uint4(0u, 0u, 0u, 0u);
         for (int idx = tid; idx < QT * NB; idx += QNTH) {
             const int i = idx / NB, bs = idx % NB;
             const size_t ar = beg + min(i, cnt - 1);
@@ -1177,10 +1178,13 @@ __global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
         }
     }
     __syncthreads();
-    // A's mask: row 2 t + hh keeps half hh, bytes 16 hh .. 16 hh + 15, which
-    // lanes kq = 2 hh and 2 hh + 1 hold
-    const uint32_t keep = ((n & 1) == (kq >> 1)) ? ~0u : 0u;
+    // A row 2 t + hh keeps only half hh, bytes 16 hh .. 16 hh + 15: lanes
+    // kq = 2 hh and 2 hh + 1 read them, the other lanes the row of zeros
+    // (no masking per block)
+    const bool keep = (n & 1) == (kq >> 1);
     const int at = n >> 1; // A row's input row within the 8-row group
+    const uint4 *const xrow = keep ? xq_s + at * XSTR : xq_s + QT * XSTR;
+    const int xtstr = keep ? 8 * XSTR : 0; // from one 8-row group to the next
     // acc: the sum over super-blocks of d * (the super-block's sum over its
     // blocks of d_x * isum, in asb)
     float acc[QT / 8][RT][2], asb[QT / 8][RT][2];
@@ -1203,9 +1207,14 @@ __global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
                 uint32_t wv[2];
 #pragma unroll
                 for (int w = 0; w < 2; w++) {
+                    // each byte's high bits 2 k, 2 k + 1 of qh moved to bits 4, 5
                     const uint32_t lo = (ql[r][pi][w][qq] >> (4 * hi)) & 0x0F0F0F0Fu;
-                    const uint32_t hb = ((qh[r][w][qq] >> (2 * k)) & 0x03030303u) << 4;
-                    wv[w] = (((lo | hb) | 0x80808080u) - 0x20202020u) ^ 0x80808080u; // bytewise q - 32
+                    const uint32_t qv = qh[r][w][qq];
+                    const uint32_t hs = k <= 2 ? qv << (4 - 2 * k) : qv >> (2 * k - 4);
+                    const uint32_t x = (hs & 0x30303030u) | lo;
+                    // bytewise q - 32: q + 96 carries out of no byte, and
+                    // flipping bit 7 then subtracts 128 mod 256
+                    wv[w] = (x + 0x60606060u) ^ 0x80808080u;
                 }
                 wo[r] = (long)((uint64_t)wv[0] | (uint64_t)wv[1] << 32);
                 const int sidx = s2 - 8 * gq; // 0..7 within the group's run
@@ -1220,8 +1229,8 @@ __global__ __launch_bounds__(QNTH) void k_q6k_down_mfma(MvArgs a)
 #pragma unroll
             for (int t = 0; t < QT / 8; t++) {
                 if (8 * t >= cnt) break; // uniform
-                const uint4 *xr = xq_s + (8 * t + at) * XSTR + 16 * g + 8 * xpi + 2 * kq;
-                const uint32_t lo = xr[0][j] & keep, hi2 = xr[1][j] & keep;
+                const uint4 *xr = xrow + t * xtstr + 16 * g + 8 * xpi + 2 * kq;
+                const uint32_t lo = xr[0][j], hi2 = xr[1][j];
                 const long xo = (long)((uint64_t)lo | (uint64_t)hi2 << 32);
                 const float2 dx = *reinterpret_cast<const float2 *>(xd_s + b * DSTR + 8 * t + 2 * kq);
 #pragma unroll
